@@ -1,0 +1,298 @@
+"""UMIC hot-path benchmark on one MI355X (BASELINE.json metric and configs).
+
+A step is one pass of the fused hot path over one batch of synthetic input at
+the BASELINE shapes, every kernel launched once through the C ABI:
+
+  rmsnorm          [3100, 4096]                     (config 2)
+  add_rmsnorm      [3100, 4096]                     (config 2)
+  layernorm        [16384, 1280] + bias             (config 2)
+  add_layernorm    [16384, 1280] + bias             (config 2)
+  rope_text        q [1,32,3100,128], k [1,8,3100,128], bf16 cos/sin (config 4)
+  rope_vision      q, k [16384,16,80] views of packed qkv, fp32 cos/sin (config 4)
+  q_proj, o_proj   [3100,4096] x [4096,4096]^T      (config 3)
+  gate_silu_mul    [3100,4096] x 2 x [12288,4096]^T (config 3, P5)
+  down_proj        [3100,12288] x [4096,12288]^T on the vendor BLAS (F.linear),
+                   as in the reference; with P5 it makes the LM MLP prefill.
+
+Inputs are resident in HBM before timing.  The HBM-bound kernels rotate over
+NSETS input sets (> 1 GB in total) so consecutive steps cannot be served from
+the 256 MB Infinity Cache.  Per-kernel durations come from HIP events
+recorded on the stream the kernels are launched on (torch's current stream),
+around each launch; the step time from a synchronised wall clock.
+
+Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
+six fused norm/RoPE kernels (algorithmic bytes / summed durations);
+mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
+(by time) of the step; cpu_baseline = the CPU oracle (scalar C, one core)
+timed on a bounded sample of the same norm/RoPE workload, in GB/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "umic-alpamayo_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+NSETS = 4
+METRIC = "fused-kernel HBM GB/s (% of peak) + LM MLP prefill ms at M=3100 bf16"
+
+
+def _bf(*shape, scale=1.0, shift=0.0, gen=None, device="cuda"):
+    import torch
+
+    return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16).to(device)
+
+
+def build_workload():
+    """Allocate every input on the GPU; return the list of kernel entries.
+
+    Entry: (name, launch(step) -> None, algorithmic bytes, flops, bound).
+    Algorithmic bytes count each tensor read or written exactly once
+    (bf16 = 2 B, fp32 = 4 B); flops are 2*M*N*K per GEMM.
+    """
+    import torch
+
+    from umic.kernels import fused_ffn, layernorm, linear, rmsnorm, rope
+
+    g = torch.Generator().manual_seed(0)
+    M, H = 3100, 4096
+    MV, HV = 16384, 1280
+    w_rms = _bf(H, scale=0.1, shift=1.0, gen=g)
+    w_ln, b_ln = _bf(HV, scale=0.1, shift=1.0, gen=g), _bf(HV, scale=0.1, gen=g)
+
+    # text RoPE tables (theta 1e6, positions 0..3099), bf16 as HF casts them
+    D = 128
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ang = torch.arange(M, dtype=torch.float32)[:, None] * inv[None]
+    emb = torch.cat((ang, ang), -1)
+    cos_t = emb.cos().to(torch.bfloat16)[None].cuda()
+    sin_t = emb.sin().to(torch.bfloat16)[None].cuda()
+    # vision RoPE tables: 16 images of 32x32 patches, merged h/w ids, theta 1e4
+    hh, ww = torch.meshgrid(torch.arange(32), torch.arange(32), indexing="ij")
+    blk = (16, 2, 16, 2)
+    hp = hh.reshape(blk).transpose(1, 2).flatten()
+    wp = ww.reshape(blk).transpose(1, 2).flatten()
+    pid = torch.stack([hp, wp], -1).repeat(16, 1)
+    vinv = 1.0 / (1e4 ** (torch.arange(0, 40, 2, dtype=torch.float32) / 40))
+    vemb = (pid[..., None].float() * vinv).flatten(1)
+    vemb = torch.cat((vemb, vemb), -1)
+    cos_v, sin_v = vemb.cos().cuda(), vemb.sin().cuda()
+
+    sets = []
+    for _ in range(NSETS):
+        s = {
+            "x": _bf(M, H, gen=g), "r": _bf(M, H, gen=g),
+            "xv": _bf(MV, HV, gen=g), "rv": _bf(MV, HV, gen=g),
+            "q": _bf(1, M, 32, D, gen=g).transpose(1, 2),
+            "k": _bf(1, M, 8, D, gen=g).transpose(1, 2),
+            "qkv": _bf(MV, 3, 16, 80, gen=g),
+        }
+        sets.append(s)
+
+    xg = _bf(M, H, gen=g)
+    wq = _bf(H, H, scale=0.02, gen=g)
+    wo = _bf(H, H, scale=0.02, gen=g)
+    wg = _bf(12288, H, scale=0.02, gen=g)
+    wu = _bf(12288, H, scale=0.02, gen=g)
+    wd = _bf(H, 12288, scale=0.02, gen=g)
+    hmid = _bf(M, 12288, gen=g)
+    eps = 1e-6
+
+    def S(i):
+        return sets[i % NSETS]
+
+    def vision(i):
+        q, k, _ = S(i)["qkv"].permute(1, 0, 2, 3).unbind(0)
+        rope.apply_rotary_vision_hip(q, k, cos_v, sin_v)
+
+    b2 = 2
+    ents = [
+        ("rmsnorm", lambda i: rmsnorm.rmsnorm_hip(S(i)["x"], w_rms, eps),
+         2 * M * H * b2 + H * b2, 0, "hbm"),
+        ("add_rmsnorm", lambda i: rmsnorm.add_rmsnorm_hip(S(i)["x"], S(i)["r"], w_rms, eps),
+         4 * M * H * b2 + H * b2, 0, "hbm"),
+        ("layernorm", lambda i: layernorm.layernorm_hip(S(i)["xv"], w_ln, b_ln, eps),
+         2 * MV * HV * b2 + 2 * HV * b2, 0, "hbm"),
+        ("add_layernorm", lambda i: layernorm.add_layernorm_hip(S(i)["xv"], S(i)["rv"], w_ln, b_ln,
+                                                                eps),
+         4 * MV * HV * b2 + 2 * HV * b2, 0, "hbm"),
+        ("rope_text", lambda i: rope.apply_rotary_text_hip(S(i)["q"], S(i)["k"], cos_t, sin_t),
+         2 * b2 * (32 + 8) * M * D + 2 * b2 * M * D, 0, "hbm"),
+        ("rope_vision", vision, 2 * b2 * 2 * 16 * MV * 80 + 2 * 4 * MV * 80, 0, "hbm"),
+        ("q_proj", lambda i: linear.linear_hip(xg, wq), (M * H + H * H + M * H) * b2,
+         2 * M * H * H, "mfma"),
+        ("o_proj", lambda i: linear.linear_hip(xg, wo), (M * H + H * H + M * H) * b2,
+         2 * M * H * H, "mfma"),
+        ("gate_silu_mul", lambda i: fused_ffn.gate_silu_mul_hip(xg, wg.t(), wu.t()),
+         (M * H + 2 * 12288 * H + M * 12288) * b2, 2 * 2 * M * 12288 * H, "mfma"),
+        ("down_proj", lambda i: torch.nn.functional.linear(hmid, wd),
+         (M * 12288 + H * 12288 + M * H) * b2, 2 * M * H * 12288, "mfma"),
+    ]
+    return ents
+
+
+def cpu_baseline(sample_s: float) -> dict:
+    """Time the CPU oracle on a bounded sample of the norm/RoPE workload."""
+    import numpy as np
+
+    import oracle
+
+    oracle._load()
+    rng = np.random.default_rng(0)
+
+    def bfr(*shape, scale=1.0, shift=0.0):
+        return oracle.bf16_from_f32((shift + scale * rng.standard_normal(shape)).astype(
+            np.float32))
+
+    # Row subsets of the GPU shapes (1/4 of the rows), repeated until the
+    # sample time is spent; bytes are counted as for the GPU kernels.
+    M, H, MV, HV, D = 3100 // 4, 4096, 16384 // 4, 1280, 128
+    x, r, w = bfr(M, H), bfr(M, H), bfr(H, scale=0.1, shift=1.0)
+    xv, rv = bfr(MV, HV), bfr(MV, HV)
+    wl, bl = bfr(HV, scale=0.1, shift=1.0), bfr(HV, scale=0.1)
+    q, k = bfr(M, 32, D), bfr(M, 8, D)
+    ct, st = bfr(M, D), bfr(M, D)
+    vq, vk = bfr(MV, 16, 80), bfr(MV, 16, 80)
+    cv = rng.standard_normal((MV, 80)).astype(np.float32)
+    sv = rng.standard_normal((MV, 80)).astype(np.float32)
+    work = [
+        (lambda: oracle.rmsnorm(x, w, 1e-6), 4 * M * H),
+        (lambda: oracle.add_rmsnorm(x, r, w, 1e-6), 8 * M * H),
+        (lambda: oracle.layernorm(xv, wl, bl, 1e-6), 4 * MV * HV),
+        (lambda: oracle.add_layernorm(xv, rv, wl, bl, 1e-6), 8 * MV * HV),
+        (lambda: (oracle.rope_text(q, ct, st), oracle.rope_text(k, ct, st)),
+         4 * 40 * M * D + 4 * M * D),
+        (lambda: (oracle.rope_vision(vq, cv, sv), oracle.rope_vision(vk, cv, sv)),
+         4 * 32 * MV * 80 + 8 * MV * 80),
+    ]
+    tot_b, tot_t, passes = 0, 0.0, 0
+    t_end = time.perf_counter() + sample_s
+    while time.perf_counter() < t_end or passes == 0:
+        for fn, nbytes in work:
+            t0 = time.perf_counter()
+            fn()
+            tot_t += time.perf_counter() - t0
+            tot_b += nbytes
+        passes += 1
+    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{passes} pass(es) of the six norm/RoPE oracle functions on 1/4 of the "
+                      f"BASELINE rows ({tot_b / passes / 1e6:.0f} MB per pass), "
+                      f"{tot_t:.1f} s of single-thread scalar C"}
+
+
+def load_traffic(name: str):
+    """Measured HBM bytes per launch from the committed rocprofv3 PMC summary
+    (profiles/traffic_<kernel>.json), or None if none was committed."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-sample-s", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
+              "path is row-parallel and would shard along M with no exchange, see DESIGN.md",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from umic import _lib
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    ents = build_workload()
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        for _, fn, *_ in ents:
+            fn(i)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in ents] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(K):
+        for j, (_, fn, *_) in enumerate(ents):
+            ev[s][j][0].record()
+            fn(s)
+            ev[s][j][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    kern = {}
+    for j, (name, _, nbytes, flops, bound) in enumerate(ents):
+        us = sum(ev[s][j][0].elapsed_time(ev[s][j][1]) for s in range(K)) / K * 1e3
+        rec = {"us": round(us, 2), "bound": bound, "bytes": nbytes}
+        rec["gbps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        if bound == "hbm":
+            rec["frac"] = round(rec["gbps"] / HBM_PEAK_GBS, 4)
+        else:
+            rec["flops"] = flops
+            rec["tflops"] = round(flops / (us * 1e-6) / 1e12, 1)
+            rec["frac"] = round(rec["tflops"] / BF16_PEAK_TFLOPS, 4)
+        kern[name] = rec
+
+    hbm = [k for k in kern.values() if k["bound"] == "hbm"]
+    agg = sum(k["bytes"] for k in hbm) / (sum(k["us"] for k in hbm) * 1e-6) / 1e9
+    mlp_ms = (kern["gate_silu_mul"]["us"] + kern["down_proj"]["us"]) / 1e3
+    dom_name = max((n for n in kern if n != "down_proj"), key=lambda n: kern[n]["us"])
+    dom = kern[dom_name]
+    if dom["bound"] == "hbm":
+        roof = {"kernel": dom_name, "bound": "hbm", "achieved": dom["gbps"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": dom["frac"]}
+    else:
+        roof = {"kernel": dom_name, "bound": "mfma", "achieved": dom["tflops"],
+                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"]}
+    roof["traffic"] = load_traffic(dom_name)
+    roof["algorithmic_bytes"] = dom["bytes"]
+
+    out = {
+        "metric": METRIC,
+        "value": round(agg, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / K * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE configs 2-4 at full size: norms [3100,4096] and "
+                               "[16384,1280], RoPE text q/k [1,32|8,3100,128] and vision "
+                               "[16384,16,80], q/o proj and P5 MLP at M=3100 K=4096 N=4096|12288",
+                   "rows_lm": 3100, "rows_vit": 16384, "input_sets": NSETS},
+        "hbm_frac": round(agg / HBM_PEAK_GBS, 4),
+        "mlp_prefill_ms": round(mlp_ms, 4),
+        "kernels": kern,
+        "roofline": roof,
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_s),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,155 @@
+/*
+ * umic_hip.h -- C ABI of libumic_hip.so, the MI355X (gfx950) kernel library
+ * behind the UMIC fused hot path.
+ *
+ * Every entry point is a plain C function over device pointers and sizes:
+ * no torch types, no allocation, no synchronisation, no host reads of device
+ * memory.  Each call enqueues its kernel(s) on `stream` (a hipStream_t passed
+ * as void*, NULL = the legacy default stream) and returns immediately, so
+ * the calls are safe inside HIP stream / graph capture.
+ *
+ * Conventions
+ *   - bf16 tensors are passed as raw 16-bit storage (uint16_t bit patterns).
+ *   - Leading dimensions / strides are in ELEMENTS, not bytes.  The innermost
+ *     dimension of every tensor is contiguous (stride 1).
+ *   - Return value: UMIC_OK (0) on success; a negative UMIC_ERR_* code when
+ *     the arguments are rejected before any launch (nothing was enqueued);
+ *     a positive hipError_t value when the launch itself failed.
+ *     umic_error_string() names either kind.  The library never aborts.
+ *   - Numerics follow the eager PyTorch / HF transformers op chains that the
+ *     reference's Triton kernels replace (rounding points noted per call).
+ *
+ * Reference interfaces (soonhong99/umic-alpamayo, path:line under src/umic/)
+ * that each call replaces are cited on its declaration.
+ */
+#ifndef UMIC_HIP_H
+#define UMIC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UMIC_OK 0
+#define UMIC_ERR_INVALID_ARG (-1)  /* null pointer, negative size, bad enum */
+#define UMIC_ERR_UNSUPPORTED (-2)  /* shape / stride / alignment not handled */
+
+/* Library version string, e.g. "umic-hip 0.1.0 gfx950". */
+const char* umic_version(void);
+
+/* Human-readable text for a return code of any entry point. */
+const char* umic_error_string(int code);
+
+/*
+ * RMSNorm over the last dim, one row of n elements per output row.
+ *   y[i,:] = bf16( w * bf16( x[i,:] * rsqrt(mean(x[i,:]^2) + eps) ) )
+ * i.e. the HF Qwen3VLTextRMSNorm chain (normalise in fp32, round to bf16,
+ * then multiply by the bf16 weight and round again).
+ * x: [rows, n] row stride ldx; w: [n]; y: [rows, n] row stride ldy.
+ * Replaces: kernels/rmsnorm.py:53-73 (rmsnorm_triton) and its kernel
+ * kernels/rmsnorm.py:32-51; caller integrate.py:134-141.
+ */
+int umic_rmsnorm_bf16(const void* x, const void* w, void* y,
+                      int64_t rows, int64_t n, int64_t ldx, int64_t ldy,
+                      float eps, void* stream);
+
+/*
+ * Residual add fused into RMSNorm.
+ *   summed = bf16(x + r);  normed = rmsnorm(summed) as above.
+ * Outputs both the normalised MLP input and the new residual stream.
+ * Replaces: kernels/rmsnorm.py:103-134 (add_rmsnorm_triton), kernel
+ * kernels/rmsnorm.py:75-101; caller integrate.py:205-206.
+ */
+int umic_add_rmsnorm_bf16(const void* x, const void* r, const void* w,
+                          void* normed, void* summed,
+                          int64_t rows, int64_t n,
+                          int64_t ldx, int64_t ldr, int64_t ldn, int64_t lds,
+                          float eps, void* stream);
+
+/*
+ * LayerNorm over the last dim with affine weight and bias (biased variance).
+ *   y = bf16( fma(w, rstd * (x - mean), b) ),  fp32 statistics.
+ * Replaces: kernels/layernorm.py:54-68 (layernorm_triton), kernel
+ * kernels/layernorm.py:30-52; caller integrate.py:234-238.
+ */
+int umic_layernorm_bf16(const void* x, const void* w, const void* b, void* y,
+                        int64_t rows, int64_t n, int64_t ldx, int64_t ldy,
+                        float eps, void* stream);
+
+/*
+ * Residual add fused into LayerNorm.
+ *   summed = bf16(x + r);  normed = layernorm(summed) as above.
+ * Replaces: kernels/layernorm.py:102-124 (add_layernorm_triton), kernel
+ * kernels/layernorm.py:70-100; callers integrate.py:581-582,589-590,602-603.
+ */
+int umic_add_layernorm_bf16(const void* x, const void* r, const void* w,
+                            const void* b, void* normed, void* summed,
+                            int64_t rows, int64_t n,
+                            int64_t ldx, int64_t ldr, int64_t ldn, int64_t lds,
+                            float eps, void* stream);
+
+/* RoPE arithmetic modes for umic_rope_qk_bf16. */
+#define UMIC_ROPE_TEXT 0   /* every op rounded to bf16 (HF apply_rotary_pos_emb) */
+#define UMIC_ROPE_VISION 1 /* fp32 math, one rounding (HF apply_rotary_pos_emb_vision) */
+
+/*
+ * Rotary position embedding of q and k in ONE launch (cos/sin read once).
+ *   out[..., d] = x[..., d] * cos[d] + rotate_half(x)[..., d] * sin[d]
+ *   rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2])
+ * Tensors are addressed as [B, S, H, D] with arbitrary element strides for
+ * the batch (sb), position (ss) and head (sh) dims; D is contiguous.
+ *   q, q_out: B x S x Hq x D; k, k_out: B x S x Hk x D (Hk may be 0, then
+ *   k / k_out are ignored);  cos, sin: B x S x D with strides (cs_sb, cs_ss).
+ * cs_fp32 = 1: cos/sin are fp32, else bf16.  mode UMIC_ROPE_TEXT requires
+ * bf16 cos/sin.  D must be even.
+ * Replaces: kernels/rope.py:62-76 (_apply_one, launched once per tensor),
+ * kernels/rope.py:78-84 (apply_rotary_vision_triton) and
+ * kernels/rope.py:86-107 (make_text_rope); kernel kernels/rope.py:30-60.
+ */
+int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void* k_out,
+                      const void* cos, const void* sin, int cs_fp32, int mode,
+                      int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+                      int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                      int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                      int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                      int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                      int64_t cs_sb, int64_t cs_ss, void* stream);
+
+/* Epilogue activations for umic_linear_bf16. */
+#define UMIC_ACT_NONE 0
+#define UMIC_ACT_GELU 1 /* exact erf GELU */
+
+/*
+ * out = act(x @ w^T + bias), bf16 in/out, fp32 accumulation on MFMA.
+ * x: [M, K] row stride ldx; w: [N, K] (nn.Linear layout) row stride ldw;
+ * bias: [N] bf16 or NULL; out: [M, N] row stride ldo.
+ * Requires K % 64 == 0, N % 8 == 0, ldx/ldw/ldo % 8 == 0 and 16-byte
+ * aligned pointers (else UMIC_ERR_UNSUPPORTED).
+ * Replaces: kernels/linear.py:118-145 (linear_triton), kernel
+ * kernels/linear.py:32-90; caller integrate.py:98-107.
+ */
+int umic_linear_bf16(const void* x, const void* w, const void* bias, void* out,
+                     int64_t M, int64_t N, int64_t K,
+                     int64_t ldx, int64_t ldw, int64_t ldo,
+                     int act, void* stream);
+
+/*
+ * Fused P5 MLP front half: out = silu(x @ wg^T) * (x @ wu^T), one bf16
+ * rounding of the fp32 product.  wg, wu: [N, K] nn.Linear weights (the
+ * reference passes them as .t() views; same memory).
+ * Same shape / alignment rules as umic_linear_bf16.
+ * Replaces: kernels/fused_ffn.py:93-126 (gate_silu_mul_triton /
+ * gate_silu_mul), kernel kernels/fused_ffn.py:48-91; caller
+ * integrate.py:44-55.
+ */
+int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void* wu,
+                            void* out, int64_t M, int64_t N, int64_t K,
+                            int64_t ldx, int64_t ldwg, int64_t ldwu,
+                            int64_t ldo, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UMIC_HIP_H */

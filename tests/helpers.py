@@ -1,0 +1,48 @@
+"""Shared test helpers: bf16 bit views, ulp metrics, seeded inputs."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """uint16 bf16 bit patterns of a bf16 tensor (any device)."""
+    assert t.dtype == torch.bfloat16, t.dtype
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def from_bits(a: np.ndarray, device="cpu") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def ulp(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """bf16 ulp distance of two uint16 bit arrays."""
+
+    def ordered(v):
+        v = np.asarray(v).astype(np.int32)
+        return np.where((v & 0x8000) != 0, -(v & 0x7FFF), v & 0x7FFF)
+
+    return np.abs(ordered(a) - ordered(b))
+
+
+def ulp_hist(d: np.ndarray, cap: int = 4) -> dict:
+    return {f"{i}": int((d == i).sum()) for i in range(cap)} | {f">={cap}": int((d >= cap).sum())}
+
+
+def bf16_randn(*shape, scale=1.0, shift=0.0, gen=None) -> torch.Tensor:
+    """N(shift, scale^2) drawn on the CPU in fp32, then rounded to bf16."""
+    return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16)
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Norm-relative error, the reference's smoke-test metric
+    (scripts/check_env.py:124-125)."""
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def max_rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    """max |a - b| / max |b| over the tensor."""
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).abs().max() / b.abs().max())

@@ -1,0 +1,126 @@
+"""The C ABI surface of libumic_hip.so, checked without a GPU.
+
+The library loads in a GPU-less process (HIP initialises lazily), exports
+every function include/umic_hip.h declares with the ctypes signature the
+Python side binds, and rejects bad arguments before any launch (those
+paths return without touching the device).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "umic_hip.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(umic_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from umic import _lib
+
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
+              "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
+              "umic_gate_silu_mul_bf16", "umic_version", "umic_error_string"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from umic import _lib
+
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes binding"
+
+
+def test_binding_arity_matches_header():
+    from umic import _lib
+
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for name, args in _lib.SIGNATURES.items():
+        m = re.search(rf"\b{name}\s*\(([^)]*)\)", text)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))
+
+
+def test_version_and_error_strings(lib):
+    from umic import _lib
+
+    assert _lib.version().startswith("umic-hip") and "gfx950" in _lib.version()
+    assert _lib.error_string(0) == "success"
+    assert "invalid" in _lib.error_string(_lib.UMIC_ERR_INVALID_ARG)
+    assert "unsupported" in _lib.error_string(_lib.UMIC_ERR_UNSUPPORTED)
+    assert _lib.error_string(-99) == "unknown umic error"
+
+
+def test_argument_rejection_before_launch(lib):
+    """Null pointers, negative sizes and unsupported shapes return an error
+    code without enqueuing anything (no device needed)."""
+    from umic import _lib
+
+    E_ARG, E_UNS = _lib.UMIC_ERR_INVALID_ARG, _lib.UMIC_ERR_UNSUPPORTED
+    fake = 1 << 20  # never dereferenced: every call below fails validation
+    assert lib.umic_rmsnorm_bf16(None, fake, fake, 4, 64, 64, 64, 1e-6, None) == E_ARG
+    assert lib.umic_rmsnorm_bf16(fake, fake, fake, -1, 64, 64, 64, 1e-6, None) == E_ARG
+    assert lib.umic_rmsnorm_bf16(fake, fake, fake, 4, 64, 32, 64, 1e-6, None) == E_ARG
+    assert lib.umic_rmsnorm_bf16(fake, fake, fake, 0, 64, 64, 64, 1e-6, None) == 0
+    assert lib.umic_add_rmsnorm_bf16(fake, None, fake, fake, fake, 4, 64, 64, 64, 64, 64,
+                                     1e-6, None) == E_ARG
+    assert lib.umic_layernorm_bf16(fake, fake, None, fake, 4, 64, 64, 64, 1e-6, None) == E_ARG
+    # linear: K not a multiple of 64, N not a multiple of 8, bad act
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 96, 96, 96, 64, 0, None) == E_UNS
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 60, 128, 128, 128, 60, 0, None) == E_UNS
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 7, None) == E_ARG
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 0, 64, 128, 128, 128, 64, 0, None) == 0
+    assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
+                                       None) == E_ARG
+    # rope: odd head dim, text mode with fp32 tables, bad mode
+    args = [fake, fake, fake, fake, fake, fake]
+    strides = [0] * 12 + [0, 0]
+    assert lib.umic_rope_qk_bf16(*args, 0, 0, 1, 4, 2, 2, 81, *strides, None) == E_UNS
+    assert lib.umic_rope_qk_bf16(*args, 1, 0, 1, 4, 2, 2, 64, *strides, None) == E_UNS
+    assert lib.umic_rope_qk_bf16(*args, 0, 5, 1, 4, 2, 2, 64, *strides, None) == E_ARG
+    assert lib.umic_rope_qk_bf16(*args, 0, 0, 1, 0, 2, 2, 64, *strides, None) == 0
+
+
+def test_wrappers_refuse_cpu_tensors():
+    import torch
+
+    from umic.kernels import layernorm, linear, rmsnorm
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        rmsnorm.rmsnorm_hip(x, w, 1e-6)
+    with pytest.raises(ValueError):
+        layernorm.layernorm_hip(x, w, w, 1e-6)
+    with pytest.raises(ValueError):
+        linear.linear_hip(x, torch.zeros(64, 64, dtype=torch.bfloat16))
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    """With the library unloadable, loading raises UmicLibraryError (the
+    wrappers call it before any launch)."""
+    from umic import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "HAS_KERNELS", False)
+    with pytest.raises(_lib.UmicLibraryError):
+        _lib.load("/nonexistent/libumic_hip.so")
+    assert not _lib.HAS_KERNELS

@@ -1,0 +1,118 @@
+"""GPU parity: MFMA linear (q/o projections) and fused P5 gate_silu_mul.
+
+Small and ragged shapes are compared with the CPU oracle (double
+accumulation, one rounding -- the fused kernels' own numerics); the
+BASELINE shapes (M=3100, K=4096: q/o N=4096, P5 N=12288) are compared with an
+fp32 torch evaluation on the same GPU.  Bar: max |err| / max |ref| <= 2e-2
+and the reference's norm-relative error (scripts/check_env.py:124) <= 2e-2;
+against the oracle the outputs must also agree to 1 bf16 ulp almost
+everywhere (only the fp32 summation order differs).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from helpers import bf16_randn, bits, from_bits, max_rel_err, rel_err, ulp
+
+import oracle
+from umic.kernels import fused_ffn, linear
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 2e-2
+
+
+def _check_vs_oracle(out, ref_bits):
+    d = ulp(bits(out), ref_bits)
+    assert (d <= 1).mean() > 0.999, np.bincount(d.ravel())[:8]
+    ref = from_bits(ref_bits)
+    assert max_rel_err(out, ref) <= TOL and rel_err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 520, 320), (256, 256, 64), (64, 8, 128), (1, 64, 256),
+                                   (513, 1024, 512), (0, 64, 64)])
+def test_linear_vs_oracle(M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.05, gen=g)
+    y = linear.linear_hip(x.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (M, N)
+    if M:
+        _check_vs_oracle(y, oracle.linear(bits(x), bits(w), None, 0, fused=True))
+
+
+def test_linear_bias_gelu_vs_oracle():
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 200, 392, 192
+    x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.1, gen=g)
+    b = bf16_randn(N, scale=0.5, gen=g)
+    for act in (None, "gelu"):
+        y = linear.linear_hip(x.to(DEV), w.to(DEV), b.to(DEV), act=act)
+        torch.cuda.synchronize()
+        _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), 1 if act else 0, fused=True))
+
+
+def test_linear_strided_x_and_leading_dims():
+    g = torch.Generator().manual_seed(4)
+    big = bf16_randn(2, 70, 512 + 64, gen=g)
+    w = bf16_randn(136, 512, scale=0.05, gen=g)
+    x = big[..., :512]                     # row stride 576, leading dims [2, 70]
+    y = linear.linear_hip(big.to(DEV)[..., :512], w.to(DEV))
+    assert y.shape == (2, 70, 136)
+    _check_vs_oracle(y.reshape(-1, 136), oracle.linear(bits(x.reshape(-1, 512)), bits(w), None,
+                                                       0, fused=True))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 520, 320), (64, 128, 64), (257, 384, 1024), (1, 8, 64)])
+def test_gate_silu_mul_vs_oracle(M, N, K):
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    x = bf16_randn(M, K, gen=g)
+    wg, wu = bf16_randn(N, K, scale=0.05, gen=g), bf16_randn(N, K, scale=0.05, gen=g)
+    y = fused_ffn.gate_silu_mul_hip(x.to(DEV), wg.to(DEV).t(), wu.to(DEV).t())
+    torch.cuda.synchronize()
+    _check_vs_oracle(y, oracle.gate_silu_mul(bits(x), bits(wg), bits(wu), fused=True))
+    # and within the bar of the eager (bf16 per-op) chain
+    eager = from_bits(oracle.gate_silu_mul(bits(x), bits(wg), bits(wu), fused=False))
+    assert max_rel_err(y, eager) <= TOL and rel_err(y, eager) <= TOL
+
+
+def test_gate_silu_mul_row_major_kn_weights():
+    """A genuinely [K, N] row-major weight (not a .t() view) is accepted."""
+    g = torch.Generator().manual_seed(5)
+    x = bf16_randn(70, 128, gen=g)
+    wg_kn, wu_kn = bf16_randn(128, 64, scale=0.1, gen=g), bf16_randn(128, 64, scale=0.1, gen=g)
+    y = fused_ffn.gate_silu_mul(x.to(DEV), wg_kn.to(DEV), wu_kn.to(DEV))
+    _check_vs_oracle(y, oracle.gate_silu_mul(bits(x), bits(wg_kn.t()), bits(wu_kn.t())))
+
+
+def _fp32_ref_linear(x, w):
+    return (x.float() @ w.float().t())
+
+
+def test_qo_projection_full_shape():
+    """q_proj / o_proj at M=3100, K=N=4096."""
+    torch.manual_seed(0)
+    x = torch.randn(3100, 4096).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(4096, 4096) * 0.02).to(torch.bfloat16).to(DEV)
+    y = linear.linear_hip(x, w)
+    ref = _fp32_ref_linear(x, w)
+    e1, e2 = max_rel_err(y, ref), rel_err(y, ref)
+    print(f"q/o proj: max_rel {e1:.2e} rel {e2:.2e}", flush=True)
+    assert e1 <= TOL and e2 <= TOL
+
+
+def test_p5_full_shape():
+    """gate_silu_mul at M=3100, K=4096, N=12288."""
+    torch.manual_seed(0)
+    x = torch.randn(3100, 4096).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(12288, 4096) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(12288, 4096) * 0.02).to(torch.bfloat16).to(DEV)
+    y = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
+    gate = x.float() @ wg.float().t()
+    ref = torch.nn.functional.silu(gate) * (x.float() @ wu.float().t())
+    del gate
+    e1, e2 = max_rel_err(y, ref), rel_err(y, ref)
+    print(f"P5: max_rel {e1:.2e} rel {e2:.2e}", flush=True)
+    assert e1 <= TOL and e2 <= TOL

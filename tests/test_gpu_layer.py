@@ -1,0 +1,124 @@
+"""GPU: a full Qwen3-VL decoder layer and a small ViT through umic.apply-style
+injection (hidden 4096, 32 q / 8 kv heads, head_dim 128,
+intermediate 12288, random N(0, 0.02) weights, norms 1 + N(0, 0.1)).
+
+Prefill (M=3100) must take every fused kernel -- checked by counting the C-ABI
+calls -- and decode (M=1) must keep the GEMM sites on the vendor path
+(FUSE_MIN_ROWS) while norms and RoPE stay fused.  Outputs are compared with the
+unpatched layer on the same GPU within the GEMM tolerance.
+"""
+
+from __future__ import annotations
+
+import collections
+
+import pytest
+import torch
+from helpers import max_rel_err, rel_err
+
+from umic import _lib, integrate
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::FutureWarning")]
+DEV = "cuda"
+TOL = 2e-2
+
+
+@pytest.fixture
+def call_log(monkeypatch):
+    log = collections.Counter()
+    real = _lib.call
+
+    def spy(name, *args):
+        log[name] += 1
+        return real(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    yield log
+    integrate.unfuse_rope()
+
+
+def decoder_layer():
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextDecoderLayer,
+                                                                Qwen3VLTextRotaryEmbedding)
+
+    cfg = Qwen3VLTextConfig(hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                            num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                            rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+                            attn_implementation="sdpa")
+    torch.manual_seed(0)
+    layer = Qwen3VLTextDecoderLayer(cfg, 0)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                p.copy_(1 + 0.1 * torch.randn_like(p))
+            else:
+                p.copy_(0.02 * torch.randn_like(p))
+    rot = Qwen3VLTextRotaryEmbedding(cfg)
+    return layer.to(torch.bfloat16).to(DEV).eval(), rot.to(DEV)
+
+
+@pytest.mark.parametrize("M", [3100, 1])
+def test_decoder_layer_prefill_and_decode(M, call_log):
+    layer, rot = decoder_layer()
+    torch.manual_seed(1)
+    h = torch.randn(1, M, 4096).to(torch.bfloat16).to(DEV)
+    pos = torch.arange(M, device=DEV)[None]
+    cos_sin = rot(h, pos)
+    with torch.no_grad():
+        ref = layer(h, position_embeddings=cos_sin)
+        assert integrate.fuse_mlps(layer) == 1
+        assert integrate.fuse_linears(layer) == 2
+        assert integrate.fuse_rmsnorms(layer) == 4
+        assert integrate.fuse_add_rmsnorm(layer) == 1
+        assert integrate.fuse_text_rope()
+        out = layer(h, position_embeddings=cos_sin)
+        torch.cuda.synchronize()
+    e1, e2 = max_rel_err(out, ref), rel_err(out, ref)
+    print(f"decoder layer M={M}: max_rel {e1:.2e} rel {e2:.2e} calls {dict(call_log)}",
+          flush=True)
+    assert e1 <= TOL and e2 <= TOL
+    assert call_log["umic_rmsnorm_bf16"] == 3          # input_layernorm, q_norm, k_norm
+    assert call_log["umic_add_rmsnorm_bf16"] == 1
+    assert call_log["umic_rope_qk_bf16"] == 1          # q and k in one launch
+    gemm_calls = 1 if M >= integrate.FUSE_MIN_ROWS else 0
+    assert call_log["umic_gate_silu_mul_bf16"] == gemm_calls
+    assert call_log["umic_linear_bf16"] == 2 * gemm_calls
+
+
+def test_vision_pipeline_on_gpu(call_log):
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionModel
+
+    cfg = Qwen3VLVisionConfig(depth=4, hidden_size=1280, num_heads=16, intermediate_size=2560,
+                              patch_size=16, temporal_patch_size=2, in_channels=3,
+                              spatial_merge_size=2, out_hidden_size=2048,
+                              num_position_embeddings=2304, deepstack_visual_indexes=[1],
+                              attn_implementation="sdpa")
+    torch.manual_seed(0)
+    m = Qwen3VLVisionModel(cfg).to(torch.bfloat16)
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, torch.nn.LayerNorm):
+                mod.weight.add_(0.1 * torch.randn_like(mod.weight))
+                mod.bias.add_(0.1 * torch.randn_like(mod.bias))
+    m = m.to(DEV).eval()
+    grid = torch.tensor([[1, 32, 32]] * 4, device=DEV)
+    px = torch.randn(4 * 32 * 32, 3 * 2 * 16 * 16).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        ref = m(px, grid_thw=grid)
+        integrate.fuse_layernorms(m)
+        assert integrate.fuse_vision_rope()
+        assert integrate.fuse_vision_encoder_pipeline(m) == 1
+        out = m(px, grid_thw=grid)
+        torch.cuda.synchronize()
+    for a, b in ((out.last_hidden_state, ref.last_hidden_state),
+                 (out.pooler_output, ref.pooler_output),
+                 (out.deepstack_features[0], ref.deepstack_features[0])):
+        assert max_rel_err(a, b) <= TOL and rel_err(a, b) <= TOL, (max_rel_err(a, b),
+                                                                   rel_err(a, b))
+    # 4 blocks: norm1 of block 0 plain, 3 cross-block + 4 intra-block + merger
+    # add+LN; the deepstack tap after block 1 keeps its plain add.
+    assert call_log["umic_rope_qk_bf16"] == 4
+    assert call_log["umic_add_layernorm_bf16"] == 4 + 2 + 1
+    assert call_log["umic_layernorm_bf16"] == 2 + 1   # block 0 and 2 norm1, deepstack merger

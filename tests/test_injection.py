@@ -1,0 +1,282 @@
+"""Injection semantics on real transformers module trees, on the CPU.
+
+Mirrors the reference's structural contract (src/umic/integrate.py,
+src/umic/optimize.py): duck-typed matching with dry-run counts, forward
+swap by instance attribute, weights shared (no copy), non-matching models
+untouched, FUSE_MIN_ROWS regime dispatch for the GEMM sites, idempotent
+RoPE swaps, and the original eager math for every input the fused kernels
+do not take (here: CPU tensors) -- bit-identical to the unpatched model.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+from umic import integrate, optimize
+from umic.kernels import fused_ffn, linear
+
+pytestmark = pytest.mark.filterwarnings("ignore::FutureWarning")
+
+BF = torch.bfloat16
+
+
+def tiny_text_model(layers=2, dtype=BF):
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel
+
+    cfg = Qwen3VLTextConfig(hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                            num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                            vocab_size=64, rope_parameters={"rope_type": "default",
+                                                            "rope_theta": 1e6},
+                            attn_implementation="sdpa")
+    torch.manual_seed(0)
+    return Qwen3VLTextModel(cfg).to(dtype).eval()
+
+
+def tiny_vision_model(dtype=BF):
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionModel
+
+    cfg = Qwen3VLVisionConfig(depth=4, hidden_size=64, num_heads=4, intermediate_size=128,
+                              patch_size=4, temporal_patch_size=2, in_channels=3,
+                              spatial_merge_size=2, out_hidden_size=96,
+                              num_position_embeddings=64, deepstack_visual_indexes=[1],
+                              attn_implementation="sdpa")
+    torch.manual_seed(0)
+    m = Qwen3VLVisionModel(cfg).to(dtype).eval()
+    with torch.no_grad():  # non-trivial LayerNorm affine params
+        for mod in m.modules():
+            if isinstance(mod, nn.LayerNorm):
+                mod.weight.add_(0.1 * torch.randn_like(mod.weight))
+                mod.bias.add_(0.1 * torch.randn_like(mod.bias))
+    return m
+
+
+def text_inputs(model, S=80, dtype=BF):
+    torch.manual_seed(1)
+    h = torch.randn(1, S, model.config.hidden_size).to(dtype)
+    pos = torch.arange(S)[None]
+    return dict(inputs_embeds=h, position_ids=pos)
+
+
+@pytest.fixture(autouse=True)
+def _restore_rope():
+    yield
+    integrate.unfuse_rope()
+
+
+# ---- matching and counts ---------------------------------------------------
+
+def test_dry_run_counts_and_no_patch():
+    m = tiny_text_model()
+    assert integrate.fuse_mlps(m, dry_run=True) == 2
+    assert integrate.fuse_linears(m, dry_run=True) == 4       # q_proj, o_proj x 2
+    assert integrate.fuse_rmsnorms(m, dry_run=True) == 9      # 4 per layer + final
+    assert integrate.fuse_add_rmsnorm(m, dry_run=True) == 2
+    assert not any("forward" in mod.__dict__ for mod in m.modules())
+
+
+def test_patch_binds_instance_forward_and_unfuse_restores():
+    m = tiny_text_model()
+    n = (integrate.fuse_mlps(m) + integrate.fuse_linears(m) + integrate.fuse_rmsnorms(m)
+         + integrate.fuse_add_rmsnorm(m))
+    patched = [mod for mod in m.modules() if "forward" in mod.__dict__]
+    assert len(patched) == n == 17
+    assert m.layers[0].mlp.forward.__func__ is integrate._fused_mlp_forward
+    assert integrate.unfuse_mlps(m) == 17
+    assert not any("forward" in mod.__dict__ for mod in m.modules())
+
+
+def test_weights_shared_not_copied():
+    m = tiny_text_model()
+    before = {k: (v.data_ptr(), v.clone()) for k, v in m.state_dict().items()}
+    optimize.apply(_wrap(lm=m))
+    for k, v in m.state_dict().items():
+        assert v.data_ptr() == before[k][0], k
+        assert torch.equal(v, before[k][1]), k
+
+
+def test_non_matching_model_is_noop():
+    m = nn.Sequential(nn.Linear(8, 8), nn.ReLU(), nn.LayerNorm(8, elementwise_affine=False))
+    assert integrate.fuse_mlps(m) == 0
+    assert integrate.fuse_linears(m) == 0
+    assert integrate.fuse_rmsnorms(m) == 0
+    assert integrate.fuse_add_rmsnorm(m) == 0
+    assert integrate.fuse_layernorms(m) == 0
+    assert integrate.fuse_vision_encoder_pipeline(m) == 0
+    assert not any("forward" in mod.__dict__ for mod in m.modules())
+    report = optimize.apply(m)  # no .vlm: LM fusions skipped, nothing patched
+    assert all(v in (False, True) for v in report.values())
+    assert not any("forward" in mod.__dict__ for mod in m.modules())
+
+
+def test_p5_matcher_rules():
+    class MLP(nn.Module):
+        def __init__(self, act, bias=False):
+            super().__init__()
+            self.gate_proj = nn.Linear(8, 16, bias=bias)
+            self.up_proj = nn.Linear(8, 16, bias=False)
+            self.down_proj = nn.Linear(16, 8, bias=False)
+            self.act_fn = act
+
+    assert integrate._is_p5_mlp(MLP(nn.SiLU()))
+    assert not integrate._is_p5_mlp(MLP(nn.GELU()))
+    assert not integrate._is_p5_mlp(MLP(nn.SiLU(), bias=True))
+
+
+# ---- eager fallback is the original math, bit for bit ----------------------
+
+def test_cpu_patched_text_model_is_bit_identical():
+    m = tiny_text_model()
+    inp = text_inputs(m)
+    with torch.no_grad():
+        ref = m(**inp).last_hidden_state
+        integrate.fuse_mlps(m)
+        integrate.fuse_linears(m)
+        integrate.fuse_rmsnorms(m)
+        integrate.fuse_add_rmsnorm(m)
+        assert integrate.fuse_text_rope()
+        out = m(**inp).last_hidden_state
+    assert torch.equal(out, ref)
+
+
+def test_cpu_patched_vision_model_is_bit_identical():
+    m = tiny_vision_model()
+    cfg = m.config
+    grid = torch.tensor([[1, 4, 6], [1, 2, 2]])
+    n_patch = int((grid[:, 0] * grid[:, 1] * grid[:, 2]).sum())
+    torch.manual_seed(2)
+    px = torch.randn(n_patch, cfg.in_channels * cfg.temporal_patch_size * cfg.patch_size**2)
+    with torch.no_grad():
+        ref = m(px.to(BF), grid_thw=grid)
+        assert integrate.fuse_layernorms(m) == 4 * 2 + 1 + 1   # blocks, merger, deepstack merger
+        assert integrate.fuse_vision_rope()
+        assert integrate.fuse_vision_encoder_pipeline(m) == 1
+        out = m(px.to(BF), grid_thw=grid)
+        out2 = m(px.to(BF), grid_thw=grid)  # cached constants path
+    for o in (out, out2):
+        assert torch.equal(o.last_hidden_state, ref.last_hidden_state)
+        assert torch.equal(o.pooler_output, ref.pooler_output)
+        assert len(o.deepstack_features) == len(ref.deepstack_features) == 1
+        assert torch.equal(o.deepstack_features[0], ref.deepstack_features[0])
+    assert len(m._umic_ve_cache) == 2
+
+
+# ---- FUSE_MIN_ROWS regime dispatch ----------------------------------------
+
+def test_fuse_min_rows_boundary(monkeypatch):
+    """63 rows run the eager class forward; 64 rows take the fused kernel."""
+    calls = []
+
+    def fake_p5(x, wg_kn, wu_kn):
+        calls.append(("p5", x.reshape(-1, x.shape[-1]).shape[0]))
+        return fused_ffn.gate_silu_mul_eager(x, wg_kn, wu_kn)
+
+    def fake_lin(x, w, b=None, act=None):
+        calls.append(("lin", x.reshape(-1, x.shape[-1]).shape[0]))
+        return nn.functional.linear(x, w, b)
+
+    monkeypatch.setattr(fused_ffn, "p5_eligible", lambda *a: True)
+    monkeypatch.setattr(fused_ffn, "gate_silu_mul_hip", fake_p5)
+    monkeypatch.setattr(linear, "linear_eligible", lambda *a: True)
+    monkeypatch.setattr(linear, "linear_hip", fake_lin)
+    m = tiny_text_model(layers=1)
+    integrate.fuse_mlps(m)
+    integrate.fuse_linears(m)
+    mlp, q = m.layers[0].mlp, m.layers[0].self_attn.q_proj
+    for rows in (63, 64):
+        x = torch.randn(1, rows, 128).to(BF)
+        with torch.no_grad():
+            mlp(x)
+            q(x)
+    assert calls == [("p5", 64), ("lin", 64)]
+    assert integrate.FUSE_MIN_ROWS == 64
+
+
+def test_gate_silu_mul_cpu_is_eager():
+    torch.manual_seed(3)
+    x = torch.randn(16, 64).to(BF)
+    wg, wu = torch.randn(32, 64).to(BF), torch.randn(32, 64).to(BF)
+    assert torch.equal(fused_ffn.gate_silu_mul(x, wg.t(), wu.t()),
+                       fused_ffn.gate_silu_mul_eager(x, wg.t(), wu.t()))
+
+
+# ---- RoPE swap --------------------------------------------------------------
+
+def test_text_rope_swap_is_idempotent_and_falls_back():
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as hf
+
+    orig = hf.apply_rotary_pos_emb
+    assert integrate.fuse_text_rope() and integrate.fuse_text_rope()
+    fused = hf.apply_rotary_pos_emb
+    assert fused is not orig and fused.__wrapped__ is orig and fused._umic_fused
+    torch.manual_seed(4)
+    q = torch.randn(2, 3, 5, 16).to(BF)     # B = 2, [B, H, S, D]
+    cos, sin = torch.randn(2, 5, 16).to(BF), torch.randn(2, 5, 16).to(BF)
+    for kw in ({}, {"unsqueeze_dim": 1}):
+        a = fused(q, q, cos, sin, **kw)
+        b = orig(q, q, cos, sin, **kw)
+        assert all(torch.equal(x, y) for x, y in zip(a, b))
+    qs = q.transpose(1, 2)                   # [B, S, H, D] with unsqueeze_dim=2
+    a, b = fused(qs, qs, cos, sin, unsqueeze_dim=2), orig(qs, qs, cos, sin, unsqueeze_dim=2)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    assert integrate.unfuse_rope() == 1 and hf.apply_rotary_pos_emb is orig
+
+
+def test_vision_rope_swap_falls_back_on_cpu():
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as hf
+
+    orig = hf.apply_rotary_pos_emb_vision
+    assert integrate.fuse_vision_rope()
+    torch.manual_seed(5)
+    q = torch.randn(10, 2, 20).to(BF)
+    cos, sin = torch.randn(10, 20), torch.randn(10, 20)
+    a, b = hf.apply_rotary_pos_emb_vision(q, q, cos, sin), orig(q, q, cos, sin)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+# ---- apply() ---------------------------------------------------------------
+
+def _wrap(lm=None, visual=None, expert=None):
+    vlm = nn.Module()
+    if lm is not None:
+        vlm.language_model = lm
+    if visual is not None:
+        vlm.visual = visual
+    root = nn.Module()
+    root.vlm = vlm
+    if expert is not None:
+        root.expert = expert
+    return root
+
+
+def test_apply_report():
+    model = _wrap(lm=tiny_text_model(), visual=tiny_vision_model(),
+                  expert=tiny_text_model(layers=1))
+    report = optimize.apply(model)
+    assert report["lm_mlp_fused"] == 2 and report["lm_linear_fused"] == 4
+    assert report["lm_rmsnorm_fused"] == 9 and report["lm_add_rmsnorm_fused"] == 2
+    assert report["text_rope_fused"] is True
+    assert report["ve_layernorm_fused"] == 10 and report["ve_rope_fused"] is True
+    assert report["ve_pipeline_fused"] == 1
+    assert report["expert_rmsnorm_fused"] == 5 and report["expert_add_rmsnorm_fused"] == 1
+    assert report["decode_graph"] is False and report["flow_cache_hook"] is False
+    cfg = optimize.UmicConfig(mlp_fusion=False, vision_fusion=False, decode_graph=False,
+                              flow_cache=False, decode_cache=False)
+    report2 = optimize.apply(_wrap(lm=tiny_text_model()), cfg)
+    assert "lm_mlp_fused" not in report2 and "ve_layernorm_fused" not in report2
+    assert "decode_graph" not in report2
+
+
+def test_find_lm_module_variants():
+    lm = tiny_text_model(layers=1)
+    assert optimize.find_lm_module(_wrap(lm=lm)) is lm
+    outer = nn.Module()
+    outer.model = lm
+    root = nn.Module()
+    root.vlm = nn.Module()
+    root.vlm.language_model = outer
+    assert optimize.find_lm_module(root) is outer
+    assert optimize.find_lm_module(nn.Linear(2, 2)) is None

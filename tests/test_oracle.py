@@ -1,0 +1,341 @@
+"""Pin the CPU oracle (oracle/umic_oracle.c) before trusting it as the checker.
+
+Every oracle function is checked against (a) the golden fixtures written by
+tests/golden/make_golden.py from the eager transformers/torch functions the
+reference's kernels replace, (b) the same library routines on fresh random
+inputs, and (c) properties the mathematics fixes (exact scale invariance,
+constant rows, position-0 identity, complex rotation, fp64 GEMM).  Several
+checks are chosen to fail on a plausible mistake -- e.g. rounding once
+instead of at the eager chain's two rounding points.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from helpers import bf16_randn, bits, from_bits, rel_err, ulp
+
+pytestmark = pytest.mark.filterwarnings("ignore::FutureWarning")
+
+
+def f32(o, a):
+    return o.f32_from_bf16(a)
+
+
+# ---- bf16 rounding --------------------------------------------------------
+
+def test_bf16_rounding_matches_torch(oracle_lib):
+    o = oracle_lib
+    rng = np.random.default_rng(0)
+    u = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    # add exact ties, denormals, max finite, infinities
+    ties = (rng.integers(0, 2**16, size=4096, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    extra = np.array([0x00000001, 0x00008000, 0x00018000, 0x7F7FFFFF, 0x7F7F8000,
+                      0x7F800000, 0xFF800000, 0x80000000, 0x3F808000, 0x3F818000],
+                     dtype=np.uint32)
+    u = np.concatenate([u, ties, extra])
+    f = u.view(np.float32)
+    finite = np.isfinite(f) | np.isinf(f)
+    f = f[finite & ~np.isnan(f)]
+    ours = o.bf16_from_f32(f)
+    ref = bits(torch.from_numpy(f.copy()).to(torch.bfloat16))
+    assert np.array_equal(ours, ref)
+
+
+# ---- RMSNorm --------------------------------------------------------------
+
+def _hf_rmsnorm(x, w, eps):
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextRMSNorm
+
+    m = Qwen3VLTextRMSNorm(x.shape[-1], eps=eps).to(torch.bfloat16)
+    with torch.no_grad():
+        m.weight.copy_(w)
+        return m(x)
+
+
+def test_rmsnorm_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    y = o.rmsnorm(g["rms_x"], g["rms_w"], 1e-6)
+    assert np.array_equal(y, g["rms_y"])
+    yq = o.rmsnorm(g["rmsq_x"], g["rmsq_w"], 1e-6)
+    assert np.array_equal(yq, g["rmsq_y"])
+
+
+def test_rmsnorm_single_rounding_would_fail(oracle_lib, golden):
+    """The golden data separates the eager double rounding from a one-rounding
+    formula (the reference Triton kernel's, kernels/rmsnorm.py:49)."""
+    o, g = oracle_lib, golden
+    x = f32(o, g["rms_x"]).astype(np.float64)
+    w = f32(o, g["rms_w"]).astype(np.float64)
+    rstd = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6)
+    once = o.bf16_from_f32((x * rstd * w).astype(np.float32))
+    frac_diff = (ulp(once, g["rms_y"]) > 0).mean()
+    assert frac_diff > 0.05, frac_diff
+
+
+def test_rmsnorm_vs_hf_random(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(1)
+    for rows, n, scale in ((128, 4096, 1.0), (300, 1280, 3.0), (512, 128, 0.01)):
+        x = bf16_randn(rows, n, scale=scale, gen=gen)
+        w = bf16_randn(n, scale=0.1, shift=1.0, gen=gen)
+        ref = bits(_hf_rmsnorm(x, w, 1e-6))
+        d = ulp(o.rmsnorm(bits(x), bits(w), 1e-6), ref)
+        # Torch's fp32 mean can differ from the exact one by a few fp32 ulps,
+        # which flips a bf16 rounding only on near-ties.
+        assert d.max() <= 2 and (d == 0).mean() > 0.999, (n, d.max(), (d > 0).sum())
+
+
+def test_rmsnorm_scale_invariance_exact(oracle_lib):
+    """eps = 0: scaling a row by 2^k scales rstd by exactly 2^-k."""
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(2)
+    x = bf16_randn(64, 1024, gen=gen)
+    w = bf16_randn(1024, scale=0.1, shift=1.0, gen=gen)
+    y = o.rmsnorm(bits(x), bits(w), 0.0)
+    for k in (-3, 5):
+        xs = bits((x.float() * 2.0**k).to(torch.bfloat16))
+        assert np.array_equal(o.rmsnorm(xs, bits(w), 0.0), y)
+
+
+def test_rmsnorm_constant_row(oracle_lib):
+    o = oracle_lib
+    n = 256
+    x = np.full((3, n), 0, np.uint16)
+    vals = [1.5, -0.25, 3.0]
+    for i, v in enumerate(vals):
+        x[i] = bits(torch.full((n,), v, dtype=torch.bfloat16))
+    w = bits(torch.linspace(0.5, 1.5, n).to(torch.bfloat16))
+    y = f32(o, o.rmsnorm(x, w, 0.0))
+    wf = f32(o, w)
+    for i, v in enumerate(vals):
+        assert np.array_equal(y[i], f32(o, o.bf16_from_f32(np.sign(v) * wf)))
+
+
+def test_add_rmsnorm_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    normed, summed = o.add_rmsnorm(g["rms_x"], g["rms_r"], g["rms_w"], 1e-6)
+    assert np.array_equal(summed, g["addrms_s"])
+    assert np.array_equal(normed, g["addrms_y"])
+
+
+# ---- LayerNorm -------------------------------------------------------------
+
+def _ln_close(o, ours, ref, w, b, x_rows_scale=1.0):
+    """<= 1 ulp, except where w*t and b nearly cancel: there the bf16 ulp of
+    the result is far below the rounding error of the fp32 terms, so allow
+    1 ulp of the larger term's magnitude instead."""
+    d = ulp(ours, ref)
+    big = d > 1
+    if big.any():
+        a, r = f32(o, ours), f32(o, ref)
+        scale = np.abs(f32(o, b))[None, :] + np.abs(f32(o, w))[None, :] * 4.0
+        tol = scale * 2.0**-8
+        assert np.all(np.abs(a - r)[big] <= np.broadcast_to(tol, a.shape)[big])
+    return d
+
+
+def test_layernorm_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    y = o.layernorm(g["ln_x"], g["ln_w"], g["ln_b"], 1e-6)
+    d = _ln_close(o, y, g["ln_y"], g["ln_w"], g["ln_b"])
+    assert (d == 0).mean() > 0.999
+    normed, summed = o.add_layernorm(g["ln_x"], g["ln_r"], g["ln_w"], g["ln_b"], 1e-6)
+    assert np.array_equal(summed, g["addln_s"])
+    d = _ln_close(o, normed, g["addln_y"], g["ln_w"], g["ln_b"])
+    assert (d == 0).mean() > 0.999
+
+
+def test_layernorm_vs_torch_random(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(3)
+    for rows, n, shift in ((256, 1280, 0.0), (128, 1152, 2.0), (64, 4096, -0.5)):
+        x = bf16_randn(rows, n, shift=shift, gen=gen)
+        w = bf16_randn(n, scale=0.1, shift=1.0, gen=gen)
+        b = bf16_randn(n, scale=0.1, gen=gen)
+        ref = bits(torch.nn.functional.layer_norm(x, (n,), w, b, 1e-6))
+        d = _ln_close(o, o.layernorm(bits(x), bits(w), bits(b), 1e-6), ref, bits(w), bits(b))
+        assert (d == 0).mean() > 0.999, (n, (d > 0).sum())
+
+
+def test_layernorm_constant_row_is_bias(oracle_lib):
+    o = oracle_lib
+    n = 640
+    x = bits(torch.full((2, n), 0.75, dtype=torch.bfloat16))
+    w = bits(torch.linspace(0.5, 1.5, n).to(torch.bfloat16))
+    b = bits(torch.linspace(-1, 1, n).to(torch.bfloat16))
+    y = o.layernorm(x, w, b, 1e-6)
+    assert np.array_equal(y[0], b) and np.array_equal(y[1], b)
+
+
+def test_layernorm_unit_stats(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(4)
+    n = 1280
+    x = bf16_randn(32, n, scale=5.0, shift=3.0, gen=gen)
+    one = bits(torch.ones(n, dtype=torch.bfloat16))
+    zero = bits(torch.zeros(n, dtype=torch.bfloat16))
+    y = f32(o, o.layernorm(bits(x), one, zero, 0.0)).astype(np.float64)
+    assert np.abs(y.mean(-1)).max() < 1e-2
+    assert np.abs(y.var(-1) - 1).max() < 1e-2
+
+
+# ---- RoPE -------------------------------------------------------------------
+
+def test_rope_text_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    cos, sin = g["rt_cos"][0], g["rt_sin"][0]
+    for x, ref in ((g["rt_q"][0], g["rt_qo"][0]), (g["rt_k"][0], g["rt_ko"][0])):
+        assert np.array_equal(o.rope_text(x, cos, sin), ref)
+
+
+def test_rope_text_vs_hf_random(oracle_lib):
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
+
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(5)
+    S, H, D = 97, 5, 64
+    x = bf16_randn(1, S, H, D, scale=4.0, gen=gen)
+    ang = torch.rand(S, D // 2, generator=gen) * 200
+    emb = torch.cat((ang, ang), -1)
+    cos, sin = emb.cos().to(torch.bfloat16)[None], emb.sin().to(torch.bfloat16)[None]
+    ref, _ = apply_rotary_pos_emb(x.transpose(1, 2), x.transpose(1, 2), cos, sin)
+    ours = o.rope_text(bits(x[0]), bits(cos[0]), bits(sin[0]))
+    assert np.array_equal(ours, bits(ref.transpose(1, 2)[0]))
+
+
+def test_rope_text_position_zero_identity(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(6)
+    x = bits(bf16_randn(1, 8, 128, gen=gen))
+    cos = bits(torch.ones(1, 128, dtype=torch.bfloat16))
+    sin = bits(torch.zeros(1, 128, dtype=torch.bfloat16))
+    assert np.array_equal(o.rope_text(x, cos, sin), x)
+
+
+def test_rope_text_is_complex_rotation(oracle_lib):
+    """Pairs (d, d+D/2) rotate as x * e^{i theta} (fp64, bf16 tolerance)."""
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(7)
+    S, H, D = 16, 3, 128
+    x = bf16_randn(S, H, D, gen=gen)
+    th = torch.rand(S, D // 2, generator=gen) * 6.0
+    cos = torch.cat((th, th), -1).cos().to(torch.bfloat16)
+    sin = torch.cat((th, th), -1).sin().to(torch.bfloat16)
+    out = f32(o, o.rope_text(bits(x), bits(cos), bits(sin))).astype(np.float64)
+    xf = x.double().numpy()
+    c, s = cos.double().numpy()[:, None, :], sin.double().numpy()[:, None, :]
+    z = (xf[..., : D // 2] + 1j * xf[..., D // 2:]) * (c[..., : D // 2] + 1j * s[..., : D // 2])
+    ref = np.concatenate([z.real, z.imag], -1)
+    assert np.abs(out - ref).max() < 4 * 2.0**-8 * np.abs(xf).max()
+
+
+def test_rope_vision_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    for x, ref in ((g["rv_q"], g["rv_qo"]), (g["rv_k"], g["rv_ko"])):
+        assert np.array_equal(o.rope_vision(x, g["rv_cos"], g["rv_sin"]), ref)
+
+
+def test_rope_vision_vs_hf_random_and_fma_would_fail(oracle_lib):
+    """Bit-exact against HF apply_rotary_pos_emb_vision at ViT scale; a
+    contracted evaluation fma(x, cos, fl(rot * sin)) -- one rounding fewer
+    than eager's separately rounded fp32 ops -- differs on some elements."""
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb_vision
+
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(10)
+    S, H, D = 4096, 16, 80
+    q = bf16_randn(S, H, D, gen=gen)
+    th = torch.rand(S, D // 2, generator=gen) * 32
+    emb = torch.cat((th, th), -1)
+    cos, sin = emb.cos(), emb.sin()
+    ref, _ = apply_rotary_pos_emb_vision(q, q, cos, sin)
+    ours = o.rope_vision(bits(q), cos.numpy(), sin.numpy())
+    assert np.array_equal(ours, bits(ref))
+    x = q.double().numpy()
+    rot = np.concatenate([-x[..., D // 2:], x[..., : D // 2]], -1)
+    c, s = cos.double().numpy()[:, None, :], sin.double().numpy()[:, None, :]
+    b = (rot * s).astype(np.float32).astype(np.float64)
+    fused = o.bf16_from_f32((x * c + b).astype(np.float32))
+    assert (fused != ours).sum() > 0
+
+
+# ---- GEMMs ------------------------------------------------------------------
+
+def test_gemm_nt_vs_fp64(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(8)
+    x, w = bf16_randn(33, 192, gen=gen), bf16_randn(70, 192, scale=0.02, gen=gen)
+    ours = o.gemm_nt_f32(bits(x), bits(w)).astype(np.float64)
+    ref = x.double().numpy() @ w.double().numpy().T
+    assert np.abs(ours - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def test_gate_silu_mul_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    eager = o.gate_silu_mul(g["mlp_x"], g["mlp_wg"], g["mlp_wu"], fused=False)
+    d = ulp(eager, g["mlp_h"])
+    assert (d == 0).mean() > 0.98 and d.max() <= 2
+    fused = from_bits(o.gate_silu_mul(g["mlp_x"], g["mlp_wg"], g["mlp_wu"], fused=True))
+    assert rel_err(fused, from_bits(g["mlp_h"])) < 1e-2
+    # silu(0) = 0: a zero gate weight row zeroes the output column
+    wg = g["mlp_wg"].copy()
+    wg[5] = 0
+    assert np.all(f32(o, o.gate_silu_mul(g["mlp_x"], wg, g["mlp_wu"]))[:, 5] == 0)
+
+
+def test_gate_silu_mul_linear_in_up(oracle_lib, golden):
+    """Doubling W_up doubles every output exactly (power-of-two scaling)."""
+    o, g = oracle_lib, golden
+    wu2 = bits((from_bits(g["mlp_wu"]).float() * 2).to(torch.bfloat16))
+    a = f32(o, o.gate_silu_mul(g["mlp_x"], g["mlp_wg"], g["mlp_wu"]))
+    b = f32(o, o.gate_silu_mul(g["mlp_x"], g["mlp_wg"], wu2))
+    assert np.array_equal(2 * a, b)
+
+
+def test_linear_golden(oracle_lib, golden):
+    o, g = oracle_lib, golden
+    y = o.linear(g["mlp_x"], g["lin_w"], g["lin_b"], act=0, fused=False)
+    d = ulp(y, g["lin_y"])
+    assert (d == 0).mean() > 0.98 and d.max() <= 2
+
+
+def test_linear_gelu_vs_torch(oracle_lib):
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(9)
+    x, w = bf16_randn(40, 128, gen=gen), bf16_randn(64, 128, scale=0.1, gen=gen)
+    b = bf16_randn(64, scale=0.1, gen=gen)
+    ref = torch.nn.functional.gelu(x.double() @ w.double().T + b.double())
+    ours = from_bits(o.linear(bits(x), bits(w), bits(b), act=1, fused=True))
+    assert rel_err(ours, ref) < 5e-3
+
+
+def test_reference_smoke_formulas(oracle_lib):
+    """The reference's only numeric check (scripts/check_env.py:116-171,
+    seed 0, rel-err < 2e-2) restated on the oracle at a reduced row count."""
+    o = oracle_lib
+    torch.manual_seed(0)
+    M, H, I = 64, 4096, 1024
+    x = torch.randn(M, H).to(torch.bfloat16)
+    wg = (torch.randn(H, I) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(H, I) * 0.02).to(torch.bfloat16)
+    ref = torch.nn.functional.silu(x.float() @ wg.float()) * (x.float() @ wu.float())
+    ours = from_bits(o.gate_silu_mul(bits(x), bits(wg.t()), bits(wu.t())))
+    assert rel_err(ours, ref) < 2e-2
+    wn = torch.randn(H).to(torch.bfloat16)
+    ref = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(
+        torch.bfloat16) * wn
+    assert rel_err(from_bits(o.rmsnorm(bits(x), bits(wn), 1e-6)), ref) < 2e-2
+    res = torch.randn_like(x, dtype=torch.float32).to(torch.bfloat16)
+    summed = x.float() + res.float()
+    ref_h = (summed * torch.rsqrt(summed.pow(2).mean(-1, keepdim=True) + 1e-6)).to(
+        torch.bfloat16) * wn
+    nh, ns = o.add_rmsnorm(bits(x), bits(res), bits(wn), 1e-6)
+    assert max(rel_err(from_bits(nh), ref_h), rel_err(from_bits(ns), summed)) < 2e-2
+    W = 1152
+    xv = torch.randn(4096 // 8, W).to(torch.bfloat16)
+    gam = torch.randn(W).to(torch.bfloat16)
+    bet = torch.randn(W).to(torch.bfloat16)
+    ref = torch.nn.functional.layer_norm(xv.float(), (W,), gam.float(), bet.float(), 1e-6)
+    assert rel_err(from_bits(o.layernorm(bits(xv), bits(gam), bits(bet), 1e-6)), ref) < 2e-2

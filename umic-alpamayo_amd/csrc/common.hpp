@@ -1,0 +1,111 @@
+// Shared device helpers for the UMIC gfx950 kernels: bf16 bit handling,
+// 16-byte vector access, wavefront reductions and launch-time argument
+// checks.  Everything here is written for CDNA4 (64-lane wavefronts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/umic_hip.h"
+
+namespace umic {
+
+constexpr int kWave = 64;
+
+// Native 16-byte vector (clang ext_vector) -- the unit of every coalesced
+// global access below (one global_load/store_dwordx4 per lane).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 <-> fp32 --------------------------------------------------------
+// bf16 values travel as raw 16-bit patterns packed two per 32-bit word
+// (element 2i in the low half, 2i+1 in the high half, little-endian order).
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 -- the rounding every eager bf16 op
+// ends with (torch's c10::BFloat16 conversion).  gfx950 does it in hardware:
+// v_cvt_pk_bf16_f32 converts two floats per instruction under the default
+// round-to-nearest-even mode with fp32 denormals preserved, which is what
+// clang emits for a float -> __bf16 conversion.  (A NaN input yields a quiet
+// NaN; only its payload bits may differ from torch's.)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// fp32 value of bf16(f)
+__device__ __forceinline__ float rbf(float f) { return (float)(__bf16)f; }
+
+// 8 bf16 values <-> 8 floats
+__device__ __forceinline__ void unpack8(const u32x4& v, float f[8]) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z); f[5] = bf_hi(v.z);
+  f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+  u32x4 v;
+  v.x = pack2(f[0], f[1]);
+  v.y = pack2(f[2], f[3]);
+  v.z = pack2(f[4], f[5]);
+  v.w = pack2(f[6], f[7]);
+  return v;
+}
+
+// ---- streaming global access ---------------------------------------------
+// Activations are touched exactly once per kernel: load/store them with the
+// non-temporal hint so they do not evict reused data (weights, cos/sin).
+
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
+  return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ void st_stream(u32x4* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, p);
+}
+
+// ---- wavefront reductions -------------------------------------------------
+// Butterfly sum over aligned groups of G lanes (G a power of two <= 64);
+// every lane of the group ends with the group total.
+
+template <int G>
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Correctly rounded fp32 1/sqrt(v): evaluated in double, rounded once.
+__device__ __forceinline__ float rsqrt_cr(float v) {
+  return (float)(1.0 / __builtin_sqrt((double)v));
+}
+
+// ---- host-side argument checks -------------------------------------------
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Status of the launch just enqueued (0 on success).
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? UMIC_OK : (int)e;
+}
+
+}  // namespace umic

@@ -1,0 +1,237 @@
+// Rotary position embedding for q and k in one gfx950 launch.
+//
+//   out[d]        = x[d]        * cos[d]        - x[d + D/2] * sin[d]
+//   out[d + D/2]  = x[d + D/2]  * cos[d + D/2]  + x[d]       * sin[d + D/2]
+// (HF rotate_half convention).  A work item owns one head row's pair of
+// VEC-element chunks, [c*VEC, c*VEC+VEC) and the same chunk shifted by D/2,
+// so both halves of every rotation pair are in the same lane: no partner
+// gather, no cross-lane traffic.  Consecutive items walk the chunks of a
+// head, then the heads of a position, so each load/store instruction of a
+// wavefront covers whole contiguous head rows of q (then k).
+//
+// One block serves P consecutive positions: their cos/sin rows are staged
+// once into LDS (read from HBM once for q AND k, where the reference's
+// per-tensor launches read them twice), then every q and k head of those
+// positions is rotated from registers.  Activations are streamed with
+// non-temporal loads/stores: each element is read once and written once.
+//
+// Arithmetic modes (no fp contraction anywhere in this library):
+//   TEXT   -- every op rounds to bf16, as the eager bf16 chain does:
+//             bf16( bf16(x*cos) + bf16(rot*sin) )   (cos/sin bf16)
+//   VISION -- fp32 ops, one final rounding: bf16( x*cos + rot*sin ) with the
+//             two products and the sum each rounded in fp32 (HF's q.float()
+//             path; cos/sin fp32, or bf16 widened exactly).
+#include "common.hpp"
+
+namespace umic {
+namespace {
+
+struct RopeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  uint16_t* qo;
+  uint16_t* ko;
+  const void* cos;
+  const void* sin;
+  int64_t B, S, Hq, Hk, D;
+  int64_t q_sb, q_ss, q_sh, k_sb, k_ss, k_sh;
+  int64_t qo_sb, qo_ss, qo_sh, ko_sb, ko_ss, ko_sh;
+  int64_t cs_sb, cs_ss;
+};
+
+constexpr int kMaxCsFloats = 4096;  // LDS budget per table (cos, sin): 16 KB each
+
+template <int VEC>
+struct Chunk;
+template <>
+struct Chunk<8> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float f[8]) {
+    unpack8(ld_stream(reinterpret_cast<const u32x4*>(p)), f);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float f[8]) {
+    st_stream(reinterpret_cast<u32x4*>(p), pack8(f));
+  }
+};
+template <>
+struct Chunk<2> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float f[2]) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    f[0] = bf_lo(w);
+    f[1] = bf_hi(w);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float f[2]) {
+    *reinterpret_cast<uint32_t*>(p) = pack2(f[0], f[1]);
+  }
+};
+
+template <>
+struct Chunk<1> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float f[1]) { f[0] = bf2f(*p); }
+  static __device__ __forceinline__ void store(uint16_t* p, const float f[1]) {
+    *p = (uint16_t)f2bf(f[0]);
+  }
+};
+
+template <int MODE, int VEC>
+__device__ __forceinline__ void rotate(const float* xl, const float* xh, const float* cl,
+                                       const float* ch, const float* sl, const float* sh,
+                                       float* ol, float* oh) {
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    if constexpr (MODE == UMIC_ROPE_TEXT) {
+      ol[e] = rbf(xl[e] * cl[e]) + rbf((-xh[e]) * sl[e]);
+      oh[e] = rbf(xh[e] * ch[e]) + rbf(xl[e] * sh[e]);
+    } else {
+      ol[e] = xl[e] * cl[e] + (-xh[e]) * sl[e];
+      oh[e] = xh[e] * ch[e] + xl[e] * sh[e];
+    }
+  }
+}
+
+template <int MODE, bool CS32, int VEC>
+__global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int P) {
+  __shared__ float cs_l[kMaxCsFloats];
+  __shared__ float sn_l[kMaxCsFloats];
+  const int64_t npos = a.B * a.S;
+  const int64_t p0 = (int64_t)blockIdx.x * P;
+  const int D = (int)a.D;
+  const int half = D / 2;
+
+  // Stage cos/sin rows of this block's positions (fp32 in LDS; bf16 widens
+  // exactly, so TEXT mode still multiplies by the bf16 values).
+  for (int i = threadIdx.x; i < P * D; i += blockDim.x) {
+    const int pp = i / D, d = i - pp * D;
+    const int64_t p = p0 + pp;
+    float c = 0.f, s = 0.f;
+    if (p < npos) {
+      int64_t b = 0, sidx = p;
+      if (a.B != 1) {
+        b = p / a.S;
+        sidx = p - b * a.S;
+      }
+      const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+      if constexpr (CS32) {
+        c = static_cast<const float*>(a.cos)[off];
+        s = static_cast<const float*>(a.sin)[off];
+      } else {
+        c = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+        s = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+      }
+    }
+    cs_l[i] = c;
+    sn_l[i] = s;
+  }
+  __syncthreads();
+
+  const int C = half / VEC;  // chunks per half row
+  const int ipp = (int)(a.Hq + a.Hk) * C;
+  const int nq = (int)a.Hq * C;
+  for (int it = threadIdx.x; it < P * ipp; it += blockDim.x) {
+    const int pp = it / ipp;
+    const int j = it - pp * ipp;
+    const int64_t p = p0 + pp;
+    if (p >= npos) break;  // items are position-major: the rest are out too
+    int64_t b = 0, sidx = p;
+    if (a.B != 1) {
+      b = p / a.S;
+      sidx = p - b * a.S;
+    }
+    const bool isq = j < nq;
+    const int jj = isq ? j : j - nq;
+    const int h = jj / C, c = jj - h * C;
+    const uint16_t* x;
+    uint16_t* o;
+    if (isq) {
+      x = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
+      o = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
+    } else {
+      x = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
+      o = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
+    }
+    const int dl = c * VEC, dh = half + c * VEC;
+    float xl[VEC], xh[VEC], ol[VEC], oh[VEC];
+    Chunk<VEC>::load(x + dl, xl);
+    Chunk<VEC>::load(x + dh, xh);
+    const float* cb = cs_l + pp * D;
+    const float* sb = sn_l + pp * D;
+    rotate<MODE, VEC>(xl, xh, cb + dl, cb + dh, sb + dl, sb + dh, ol, oh);
+    Chunk<VEC>::store(o + dl, ol);
+    Chunk<VEC>::store(o + dh, oh);
+  }
+}
+
+template <int MODE, bool CS32, int VEC>
+int launch_rope(const RopeArgs& a, hipStream_t st) {
+  const int64_t npos = a.B * a.S;
+  const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
+  // ~1280 items per block (5 per thread), bounded by the LDS tables.
+  int64_t P = (1280 + ipp - 1) / ipp;
+  if (P < 1) P = 1;
+  if (P * a.D > kMaxCsFloats) P = kMaxCsFloats / a.D;
+  const int64_t blocks = (npos + P - 1) / P;
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((rope_qk_kernel<MODE, CS32, VEC>), dim3((unsigned)blocks), dim3(256), 0, st,
+                     a, (int)P);
+  return launch_status();
+}
+
+template <int MODE, bool CS32>
+int dispatch_vec(const RopeArgs& a, int vec, hipStream_t st) {
+  if (vec == 8) return launch_rope<MODE, CS32, 8>(a, st);
+  if (vec == 2) return launch_rope<MODE, CS32, 2>(a, st);
+  return launch_rope<MODE, CS32, 1>(a, st);
+}
+
+}  // namespace
+}  // namespace umic
+
+using namespace umic;
+
+extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void* k_out,
+                                 const void* cos, const void* sin, int cs_fp32, int mode,
+                                 int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+                                 int64_t q_sb, int64_t q_ss, int64_t q_sh, int64_t k_sb,
+                                 int64_t k_ss, int64_t k_sh, int64_t qo_sb, int64_t qo_ss,
+                                 int64_t qo_sh, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                                 int64_t cs_sb, int64_t cs_ss, void* stream) {
+  if (mode != UMIC_ROPE_TEXT && mode != UMIC_ROPE_VISION) return UMIC_ERR_INVALID_ARG;
+  if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
+  if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
+  if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
+  if (Hk > 0 && (!k || !k_out)) return UMIC_ERR_INVALID_ARG;
+  if (mode == UMIC_ROPE_TEXT && cs_fp32) return UMIC_ERR_UNSUPPORTED;
+  if (D % 2 != 0 || D > kMaxCsFloats) return UMIC_ERR_UNSUPPORTED;
+  if ((Hq + Hk) * (D / 2) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
+  if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;
+
+  RopeArgs a{(const uint16_t*)q, (const uint16_t*)k, (uint16_t*)q_out, (uint16_t*)k_out,
+             cos, sin, B, S, Hq, Hk, D,
+             q_sb, q_ss, q_sh, k_sb, k_ss, k_sh,
+             qo_sb, qo_ss, qo_sh, ko_sb, ko_ss, ko_sh, cs_sb, cs_ss};
+  if (Hq == 0) a.q = a.qo = nullptr;
+  if (Hk == 0) a.k = a.ko = nullptr;
+
+  // 16-byte chunks need 8 | D/2, every stride a multiple of 8 and 16-byte
+  // aligned bases; 4-byte pairs the same with 2; single elements always work.
+  auto all_mult = [&](int64_t m) {
+    bool ok = (D / 2) % m == 0;
+    if (Hq) ok = ok && q_sb % m == 0 && q_ss % m == 0 && q_sh % m == 0 && qo_sb % m == 0 &&
+                 qo_ss % m == 0 && qo_sh % m == 0;
+    if (Hk) ok = ok && k_sb % m == 0 && k_ss % m == 0 && k_sh % m == 0 && ko_sb % m == 0 &&
+                 ko_ss % m == 0 && ko_sh % m == 0;
+    return ok;
+  };
+  auto all_aligned = [&](uintptr_t m) {
+    bool ok = true;
+    if (Hq) ok = ok && ((uintptr_t)q % m == 0) && ((uintptr_t)q_out % m == 0);
+    if (Hk) ok = ok && ((uintptr_t)k % m == 0) && ((uintptr_t)k_out % m == 0);
+    return ok;
+  };
+  const int vec = (all_mult(8) && all_aligned(16)) ? 8 : (all_mult(2) && all_aligned(4)) ? 2 : 1;
+  if (vec == 1 && !all_aligned(2)) return UMIC_ERR_UNSUPPORTED;
+
+  hipStream_t st = as_stream(stream);
+  if (mode == UMIC_ROPE_TEXT) return dispatch_vec<UMIC_ROPE_TEXT, false>(a, vec, st);
+  if (cs_fp32) return dispatch_vec<UMIC_ROPE_VISION, true>(a, vec, st);
+  return dispatch_vec<UMIC_ROPE_VISION, false>(a, vec, st);
+}

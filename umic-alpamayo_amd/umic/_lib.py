@@ -1,0 +1,152 @@
+"""ctypes binding of libumic_hip.so, the gfx950 kernel library.
+
+The C ABI (``include/umic_hip.h``) takes raw device pointers, sizes and a
+``hipStream_t``; this module owns the one process-wide handle to it and the
+glue every wrapper needs: argument marshalling, the current-stream handle
+and return-code checking.  torch is used only as the allocator and stream
+owner -- no torch types cross the boundary.
+
+``HAS_KERNELS`` is True once the library has loaded (it loads lazily on first
+use, or eagerly via :func:`load`).  A wrapper called on device tensors while
+the library is missing raises :class:`UmicLibraryError`: the fused path never
+degrades silently to something else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libumic_hip.so")
+
+UMIC_OK = 0
+UMIC_ERR_INVALID_ARG = -1
+UMIC_ERR_UNSUPPORTED = -2
+UMIC_ROPE_TEXT = 0
+UMIC_ROPE_VISION = 1
+UMIC_ACT_NONE = 0
+UMIC_ACT_GELU = 1
+
+_P, _I64, _F32, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+
+# Exported function -> argument types, exactly as declared in umic_hip.h.
+SIGNATURES: dict[str, list] = {
+    "umic_rmsnorm_bf16": [_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P],
+    "umic_add_rmsnorm_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P],
+    "umic_layernorm_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P],
+    "umic_add_layernorm_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                _F32, _P],
+    "umic_rope_qk_bf16": [_P, _P, _P, _P, _P, _P, _I, _I] + [_I64] * 5 + [_I64] * 12
+                         + [_I64] * 2 + [_P],
+    "umic_linear_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    "umic_gate_silu_mul_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "umic_version": [],
+    "umic_error_string": [_I],
+}
+
+
+class UmicLibraryError(RuntimeError):
+    """libumic_hip.so is missing or failed to load while a kernel was needed."""
+
+
+class UmicKernelError(RuntimeError):
+    """A libumic_hip.so entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with code {code}: {msg}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+HAS_KERNELS = False
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load the library (idempotent) and return the ctypes handle."""
+    global _lib, _load_error, HAS_KERNELS
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = path or os.environ.get("UMIC_HIP_LIB", LIB_PATH)
+        try:
+            lib = ctypes.CDLL(p)
+        except OSError as exc:
+            _load_error = f"cannot load {p}: {exc}"
+            raise UmicLibraryError(_load_error) from exc
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name in ("umic_version", "umic_error_string") else _I
+        _lib = lib
+        HAS_KERNELS = True
+        return lib
+
+
+def available() -> bool:
+    """True if the library is (or can be) loaded."""
+    if _lib is not None:
+        return True
+    try:
+        load()
+        return True
+    except UmicLibraryError:
+        return False
+
+
+def lib() -> ctypes.CDLL:
+    if _lib is not None:
+        return _lib
+    return load()
+
+
+def version() -> str:
+    return lib().umic_version().decode()
+
+
+def error_string(code: int) -> str:
+    return lib().umic_error_string(code).decode()
+
+
+def call(name: str, *args) -> None:
+    """Invoke entry point ``name``; raise UmicKernelError on non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != UMIC_OK:
+        raise UmicKernelError(name, rc, error_string(rc))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t handle of the current torch stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class device_of:
+    """Make t's device current for the duration of a launch (no-op if it is)."""
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = t.device.index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.idx is not None and cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def aligned16(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0

@@ -1,0 +1,480 @@
+"""Module-level fusion injection -- zero model modification.
+
+Same contract as the reference (src/umic/integrate.py): UMIC swaps the
+*forward* of matching submodules at load time.  Matching is structural
+(duck-typed), never by class, so any model exposing the motifs is covered;
+weights are shared (no copy, no quantisation, no value change); a module
+that does not match is left untouched, so applying UMIC to a model without
+the motifs is a no-op.  Patching binds an instance attribute
+(``module.forward = fn.__get__(module)``): ``nn.Module.__call__`` still runs
+hooks, and deleting the attribute restores the class forward.
+
+Each replacement forward first decides whether the fused gfx950 kernel
+reproduces the module on the given inputs (GPU bf16 tensors of a handled
+layout; for the GEMM sites also at least FUSE_MIN_ROWS rows).  If not, it
+runs the module's own class forward -- the original eager math on whatever
+device the inputs live on.  If the inputs are eligible but libumic_hip.so
+is missing, the kernel wrapper raises: the fused path never degrades
+silently.
+"""
+
+from __future__ import annotations
+
+import logging
+
+import torch
+from torch import nn
+
+from umic.kernels import fused_ffn, layernorm, linear, rmsnorm, rope
+
+logger = logging.getLogger(__name__)
+
+_SILU_NAMES = ("silu", "swish")
+
+# Below this row count the GEMM motifs run as GEMV (decode, seq=1): the
+# vendor library is the right tool there and the eager intermediates are
+# KB-scale, so the fused GEMMs are only used from this many rows up
+# (reference src/umic/integrate.py:27-30).  Norms and RoPE have no floor:
+# one fused launch always replaces several eager ones.
+FUSE_MIN_ROWS = 64
+
+# Projection sites routed to the fused linear (reference integrate.py:91).
+INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
+
+# ViT projection site list kept from the reference (integrate.py:95); not
+# used by apply().
+VIT_LINEAR_NAMES = ("qkv",)
+
+
+def _eager(module: nn.Module, *args, **kwargs):
+    """Run the module's class forward (the unpatched eager implementation)."""
+    return type(module).forward(module, *args, **kwargs)
+
+
+def _norm_eps(module: nn.Module) -> float:
+    eps = getattr(module, "variance_epsilon", None)
+    if eps is None:
+        eps = getattr(module, "eps", 1e-6)
+    return float(eps)
+
+
+def _rows(x: torch.Tensor) -> int:
+    return x.numel() // x.shape[-1] if x.dim() >= 1 and x.shape[-1] else 0
+
+
+# ---------------------------------------------------------------------------
+# P5: gate / up / down SiLU MLP
+# ---------------------------------------------------------------------------
+
+def _is_p5_mlp(module: nn.Module) -> bool:
+    """Structural match for the gate/up/down SiLU MLP motif (pattern P5)."""
+    for attr in ("gate_proj", "up_proj", "down_proj"):
+        sub = getattr(module, attr, None)
+        if not isinstance(sub, nn.Linear) or sub.bias is not None:
+            return False
+    act = getattr(module, "act_fn", None) or getattr(module, "act", None)
+    act_name = type(act).__name__.lower() if act is not None else ""
+    return any(s in act_name for s in _SILU_NAMES)
+
+
+def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """P5-fused replacement: silu(x@Wg)*(x@Wu) in one kernel, then down."""
+    wg, wu = self.gate_proj.weight, self.up_proj.weight
+    if _rows(x) < FUSE_MIN_ROWS or not fused_ffn.p5_eligible(x, wg, wu):
+        return _eager(self, x)
+    # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
+    # takes -- the kernel reads the original weight memory.
+    h = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
+    return self.down_proj(h)
+
+
+def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
+    """Swap the forward of every P5-matching MLP in `model`.
+
+    Returns:
+        Number of modules matched (and patched unless dry_run).
+    """
+    count = 0
+    for name, module in model.named_modules():
+        if _is_p5_mlp(module):
+            count += 1
+            if not dry_run:
+                module.forward = _fused_mlp_forward.__get__(module)
+                logger.info("P5 fused: %s", name)
+    logger.info("fuse_mlps: %d module(s) %s", count, "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+# ---------------------------------------------------------------------------
+# q / o projections
+# ---------------------------------------------------------------------------
+
+def _patched_linear_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """Route large-M calls to the fused linear; GEMV stays on the vendor BLAS."""
+    if _rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, self.weight, self.bias):
+        return _eager(self, x)
+    return linear.linear_hip(x, self.weight, self.bias)
+
+
+def fuse_linears(model: nn.Module, names: tuple[str, ...] = INEFFICIENT_LINEAR_NAMES,
+                 dry_run: bool = False) -> int:
+    """Swap forward of nn.Linear submodules whose attribute name matches.
+
+    Returns:
+        Number of Linear modules matched (and patched unless dry_run).
+    """
+    count = 0
+    for name, module in model.named_modules():
+        leaf = name.rsplit(".", 1)[-1]
+        if leaf in names and isinstance(module, nn.Linear):
+            count += 1
+            if not dry_run:
+                module.forward = _patched_linear_forward.__get__(module)
+    logger.info("fuse_linears(%s): %d module(s) %s", names, count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm and the decoder-layer residual fusion
+# ---------------------------------------------------------------------------
+
+def _patched_rmsnorm_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """One fused kernel replacing the eager pow/mean/rsqrt/mul/cast chain."""
+    if not rmsnorm.rmsnorm_eligible(x, self.weight):
+        return _eager(self, x)
+    return rmsnorm.rmsnorm_hip(x, self.weight, _norm_eps(self))
+
+
+def fuse_rmsnorms(model: nn.Module, dry_run: bool = False) -> int:
+    """Swap forward of every RMSNorm-family module (duck-typed).
+
+    Match: class name contains "rmsnorm" and a 1-D `weight` (covers the
+    decoder norms, q_norm / k_norm and the final norm).
+
+    Returns:
+        Number of modules matched (and patched unless dry_run).
+    """
+    count = 0
+    for name, module in model.named_modules():
+        if "rmsnorm" not in type(module).__name__.lower():
+            continue
+        w = getattr(module, "weight", None)
+        if not isinstance(w, torch.Tensor) or w.dim() != 1:
+            continue
+        count += 1
+        if not dry_run:
+            module.forward = _patched_rmsnorm_forward.__get__(module)
+    logger.info("fuse_rmsnorms: %d module(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+def _is_residual_decoder_layer(module: nn.Module) -> bool:
+    """Structural match for the pre-norm attn + MLP decoder block."""
+    return all(hasattr(module, a) for a in
+               ("input_layernorm", "post_attention_layernorm", "self_attn", "mlp"))
+
+
+def _add_rmsnorm(norm: nn.Module, x: torch.Tensor, residual: torch.Tensor):
+    """(norm(residual + x), residual + x): fused when the kernel applies."""
+    w = getattr(norm, "weight", None)
+    if ("rmsnorm" in type(norm).__name__.lower() and isinstance(w, torch.Tensor)
+            and x.shape == residual.shape and residual.dtype == x.dtype
+            and rmsnorm.rmsnorm_eligible(x, w) and residual.device == x.device):
+        return rmsnorm.add_rmsnorm_hip(x, residual, w, _norm_eps(norm))
+    summed = residual + x
+    return norm(summed), summed
+
+
+def _fused_residual_layer_forward(self, hidden_states, position_embeddings=None,
+                                  attention_mask=None, position_ids=None,
+                                  past_key_values=None, use_cache=False, **kwargs):
+    """Decoder-layer forward with the attention-residual add fused into the
+    post-attention RMSNorm: one kernel emits both the MLP input and the new
+    residual stream.  The MLP residual add stays a plain add (its consumer is
+    the next layer's input norm).  Same call signature and return value as
+    the transformers decoder layer; extra keyword arguments pass through.
+    """
+    residual = hidden_states
+    hidden_states = self.input_layernorm(hidden_states)
+    hidden_states, _ = self.self_attn(
+        hidden_states=hidden_states, attention_mask=attention_mask,
+        position_ids=position_ids, past_key_values=past_key_values,
+        use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
+    hidden_states, residual = _add_rmsnorm(self.post_attention_layernorm, hidden_states, residual)
+    hidden_states = self.mlp(hidden_states)
+    return residual + hidden_states
+
+
+def fuse_add_rmsnorm(model: nn.Module, dry_run: bool = False) -> int:
+    """Fuse the attention-residual add into post_attention_layernorm.
+
+    Returns:
+        Number of decoder layers matched (and patched unless dry_run).
+    """
+    count = 0
+    for name, module in model.named_modules():
+        if not _is_residual_decoder_layer(module):
+            continue
+        count += 1
+        if not dry_run:
+            module.forward = _fused_residual_layer_forward.__get__(module)
+    logger.info("fuse_add_rmsnorm: %d decoder layer(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm and the ViT residual fusion
+# ---------------------------------------------------------------------------
+
+def _patched_layernorm_forward(self: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
+    """One fused kernel replacing eager's LayerNorm."""
+    if not layernorm.layernorm_eligible(x, self.weight, self.bias):
+        return _eager(self, x)
+    return layernorm.layernorm_hip(x, self.weight, self.bias, self.eps)
+
+
+def fuse_layernorms(model: nn.Module, dry_run: bool = False) -> int:
+    """Swap forward of nn.LayerNorm modules (last-dim, affine with bias)."""
+    count = 0
+    for name, module in model.named_modules():
+        if (isinstance(module, nn.LayerNorm) and len(module.normalized_shape) == 1
+                and module.weight is not None and module.bias is not None):
+            count += 1
+            if not dry_run:
+                module.forward = _patched_layernorm_forward.__get__(module)
+    logger.info("fuse_layernorms: %d module(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+def _add_layernorm(norm: nn.LayerNorm, x: torch.Tensor, residual: torch.Tensor):
+    """(norm(residual + x), residual + x): fused when the kernel applies."""
+    if (isinstance(norm, nn.LayerNorm) and len(norm.normalized_shape) == 1
+            and x.shape == residual.shape and residual.dtype == x.dtype
+            and residual.device == x.device
+            and layernorm.layernorm_eligible(x, norm.weight, norm.bias)):
+        return layernorm.add_layernorm_hip(x, residual, norm.weight, norm.bias, norm.eps)
+    summed = residual + x
+    return norm(summed), summed
+
+
+def _is_deepstack_vision_encoder(module: nn.Module) -> bool:
+    """Structural match: a grid_thw-driven ViT with deepstack taps (block list
+    of pre-norm LayerNorm attn + MLP blocks, patch embed, merger, deepstack
+    mergers) -- reference integrate.py:481-506."""
+    blocks = getattr(module, "blocks", None)
+    if not blocks or len(blocks) == 0:
+        return False
+    b0 = blocks[0]
+    if not all(hasattr(b0, a) for a in ("norm1", "norm2", "attn", "mlp")):
+        return False
+    if not (isinstance(getattr(b0, "norm1", None), nn.LayerNorm)
+            and isinstance(getattr(b0, "norm2", None), nn.LayerNorm)):
+        return False
+    merger = getattr(module, "merger", None)
+    if merger is None or not all(hasattr(merger, a) for a in
+                                 ("norm", "linear_fc1", "act_fn", "linear_fc2",
+                                  "use_postshuffle_norm", "hidden_size")):
+        return False
+    return all(hasattr(module, a) for a in
+               ("patch_embed", "deepstack_merger_list", "deepstack_visual_indexes",
+                "rotary_pos_emb", "pos_embed"))
+
+
+def _vision_constants(self: nn.Module, grid_thw: torch.Tensor):
+    """grid_thw-derived inputs of the ViT forward, computed as the installed
+    transformers version computes them (modeling_qwen3_vl.py:690-713 with the
+    transformers.vision_utils helpers; the reference used the older
+    fast_pos_embed_interpolate / rot_pos_emb methods, integrate.py:547-556)."""
+    from transformers import vision_utils as vu
+
+    interp_indices, interp_weights = vu.get_vision_interpolation_indices_and_weights(
+        grid_thw, num_grid_per_side=self.num_grid_per_side, mode=self.interpolation_mode,
+        align_corners=self.interpolation_align_corners,
+        spatial_merge_size=self.config.spatial_merge_size)
+    position_ids = vu.get_vision_position_ids(grid_thw, self.spatial_merge_size)
+    cu_seqlens, max_seqlen = vu.get_vision_attention_seqlens(grid_thw, self.config)
+    pos_embeds = (self.pos_embed(interp_indices) * interp_weights[:, :, None]).sum(1)
+    rotary = self.rotary_pos_emb(position_ids)
+    rotary = rotary.reshape(rotary.shape[0], -1)
+    emb = torch.cat((rotary, rotary), dim=-1)
+    return pos_embeds, (emb.cos(), emb.sin()), cu_seqlens, max_seqlen
+
+
+def _fused_vision_encoder_forward(self: nn.Module, hidden_states: torch.Tensor,
+                                  grid_thw: torch.Tensor, **kwargs):
+    """ViT forward with a grid_thw-keyed constants cache and every eligible
+    residual add fused into the LayerNorm that consumes it.
+
+    - Constants (pos_embeds, rotary cos/sin, cu_seqlens, max_seqlen) depend
+      only on grid_thw and are recomputed only when its value changes.
+    - Residual-add + LayerNorm fusion intra-block (attn residual into norm2)
+      and cross-block (a block's MLP residual into the next block's norm1,
+      or into the merger's norm after the last block when that norm works
+      per token).  Deepstack tap layers materialise the plain add, since
+      their mergers read the summed stream.
+    Reference: integrate.py:509-611.  The eager block order is
+    h = h + attn(norm1(h)); h = h + mlp(norm2(h)) (modeling_qwen3_vl.py:
+    299-306); each fused add is that same bf16 add.
+    """
+    cache: dict = self._umic_ve_cache
+    key = tuple(grid_thw.reshape(-1).tolist())
+    if cache.get("key") != key:
+        pos_embeds, pe, cu, mx = _vision_constants(self, grid_thw)
+        cache["key"] = key
+        cache["consts"] = (pos_embeds.detach(), (pe[0].detach(), pe[1].detach()), cu, mx)
+    pos_embeds, position_embeddings, cu_seqlens, max_seqlen = cache["consts"]
+
+    hidden_states = self.patch_embed(hidden_states)
+    hidden_states = hidden_states + pos_embeds.to(hidden_states.dtype)
+    seq_len = hidden_states.shape[0]
+    hidden_states = hidden_states.reshape(seq_len, -1)
+
+    deepstack_set = self._umic_deepstack_set
+    merger = self.merger
+    deepstack_features = []
+    pending = None
+    for layer_num, blk in enumerate(self.blocks):
+        if pending is None:
+            normed1 = blk.norm1(hidden_states)
+        else:
+            normed1, hidden_states = _add_layernorm(blk.norm1, pending, hidden_states)
+            pending = None
+        attn_out = blk.attn(normed1, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen,
+                            position_embeddings=position_embeddings, **kwargs)
+        normed2, hidden_states = _add_layernorm(blk.norm2, attn_out, hidden_states)
+        mlp_out = blk.mlp(normed2)
+        if layer_num in deepstack_set:
+            hidden_states = hidden_states + mlp_out
+            idx = list(self.deepstack_visual_indexes).index(layer_num)
+            deepstack_features.append(self.deepstack_merger_list[idx](hidden_states))
+        else:
+            pending = mlp_out
+
+    if pending is not None and not merger.use_postshuffle_norm:
+        normed, hidden_states = _add_layernorm(merger.norm, pending, hidden_states)
+        x = normed.view(-1, merger.hidden_size)
+        merged = merger.linear_fc2(merger.act_fn(merger.linear_fc1(x)))
+    else:
+        if pending is not None:
+            hidden_states = hidden_states + pending
+        merged = merger(hidden_states)
+
+    out_cls = self._umic_output_cls
+    if out_cls is None:
+        return merged, deepstack_features
+    return out_cls(last_hidden_state=hidden_states, pooler_output=merged,
+                   deepstack_features=deepstack_features)
+
+
+def fuse_vision_encoder_pipeline(model: nn.Module, dry_run: bool = False) -> int:
+    """Fuse the grid_thw-driven ViT forward (constants cache + residual fusion).
+
+    Composes with fuse_layernorms / fuse_vision_rope: norm, attention and MLP
+    submodules are called as ordinary submodule calls, so whatever forward
+    is installed on them runs.
+
+    Returns:
+        Number of vision-encoder modules matched (and patched unless dry_run).
+    """
+    try:
+        from transformers.models.qwen3_vl import modeling_qwen3_vl as mod
+        out_cls = getattr(mod, "BaseModelOutputWithDeepstackFeatures", None)
+    except ImportError:
+        out_cls = None
+    count = 0
+    for name, module in model.named_modules():
+        if not _is_deepstack_vision_encoder(module):
+            continue
+        count += 1
+        if not dry_run:
+            module._umic_ve_cache = {}
+            module._umic_deepstack_set = set(module.deepstack_visual_indexes)
+            module._umic_output_cls = out_cls
+            module.forward = _fused_vision_encoder_forward.__get__(module)
+            logger.info("vision encoder pipeline fused: %s", name)
+    logger.info("fuse_vision_encoder_pipeline: %d module(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+# ---------------------------------------------------------------------------
+# RoPE (library-function swap in transformers' qwen3_vl module)
+# ---------------------------------------------------------------------------
+
+_ROPE_ORIGINALS: dict[str, object] = {}
+
+
+def _qwen3_vl_module():
+    try:
+        import transformers.models.qwen3_vl.modeling_qwen3_vl as mod
+    except ImportError:
+        return None
+    return mod
+
+
+def fuse_vision_rope() -> bool:
+    """Replace HF apply_rotary_pos_emb_vision with the fused q+k kernel
+    (eager fallback for inputs the kernel does not handle).  Idempotent."""
+    mod = _qwen3_vl_module()
+    if mod is None:
+        logger.warning("fuse_vision_rope: qwen3_vl module not found")
+        return False
+    cur = mod.apply_rotary_pos_emb_vision
+    if getattr(cur, "_umic_fused", False):
+        return True
+    _ROPE_ORIGINALS.setdefault("apply_rotary_pos_emb_vision", cur)
+    fused = rope.make_vision_rope(cur)
+    fused._umic_fused = True
+    mod.apply_rotary_pos_emb_vision = fused
+    logger.info("fuse_vision_rope: apply_rotary_pos_emb_vision -> fused kernel")
+    return True
+
+
+def fuse_text_rope() -> bool:
+    """Replace HF apply_rotary_pos_emb (text path) with the fused kernel.
+
+    The qwen3_vl module-level function serves the LM (prefill and decode)
+    and any expert built from the same text model.  Layouts the kernel does
+    not handle fall back to the original function.  Idempotent.
+    """
+    mod = _qwen3_vl_module()
+    if mod is None:
+        logger.warning("fuse_text_rope: qwen3_vl module not found")
+        return False
+    cur = mod.apply_rotary_pos_emb
+    if getattr(cur, "_umic_fused", False):
+        return True
+    _ROPE_ORIGINALS.setdefault("apply_rotary_pos_emb", cur)
+    fused = rope.make_text_rope(cur)
+    fused._umic_fused = True
+    mod.apply_rotary_pos_emb = fused
+    logger.info("fuse_text_rope: apply_rotary_pos_emb -> fused kernel")
+    return True
+
+
+def unfuse_rope() -> int:
+    """Restore the original transformers RoPE functions; returns how many."""
+    mod = _qwen3_vl_module()
+    if mod is None:
+        return 0
+    n = 0
+    for name, fn in list(_ROPE_ORIGINALS.items()):
+        if getattr(getattr(mod, name), "_umic_fused", False):
+            setattr(mod, name, fn)
+            n += 1
+        del _ROPE_ORIGINALS[name]
+    return n
+
+
+def unfuse_mlps(model: nn.Module) -> int:
+    """Restore original forwards (delete every instance forward override)."""
+    count = 0
+    for _, module in model.named_modules():
+        if "forward" in module.__dict__:
+            del module.__dict__["forward"]
+            count += 1
+    return count

@@ -1,0 +1,76 @@
+"""bf16 linear (x @ W^T [+ bias] [+ erf-GELU]) on gfx950 MFMA (libumic_hip.so).
+
+Drop-in for the reference's ``linear_triton`` (src/umic/kernels/linear.py:
+118-145): the weight is the nn.Linear [N, K] tensor, read in place (the MFMA
+kernel consumes K-contiguous rows of both operands, so there is no transpose
+and no copy).  fp32 accumulation, bias and GELU applied to the fp32
+accumulator, one bf16 rounding.  Site selection (which Linear modules use it)
+lives in umic.integrate, as in the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from umic import _lib
+from umic.kernels._common import ld, require_device, rows2d
+
+K_MULTIPLE = 64  # the kernel's K step
+N_MULTIPLE = 8   # 16-byte output runs
+
+
+def _gemm_ready(t2d: torch.Tensor) -> torch.Tensor:
+    """Row-major view with a 16-byte aligned base and row stride (else a copy)."""
+    if t2d.stride(-1) != 1 or (t2d.shape[0] > 1 and t2d.stride(0) % 8) or t2d.data_ptr() % 16:
+        t2d = t2d.contiguous()
+    return t2d
+
+
+def linear_eligible(x: torch.Tensor, weight: torch.Tensor, bias=None) -> bool:
+    """True if (x, weight, bias) can run on the HIP kernel."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and isinstance(weight, torch.Tensor)
+            and weight.dtype == torch.bfloat16 and weight.dim() == 2
+            and weight.device == x.device and x.dim() >= 1):
+        return False
+    N, K = weight.shape
+    if x.shape[-1] != K or K % K_MULTIPLE or N % N_MULTIPLE or K == 0:
+        return False
+    if bias is not None and not (bias.dtype == torch.bfloat16 and bias.dim() == 1
+                                 and bias.shape[0] == N and bias.device == x.device):
+        return False
+    return True
+
+
+def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+               act: str | None = None) -> torch.Tensor:
+    """Compute act(x @ weight.T + bias).
+
+    Args:
+        x: [..., K] activations, bf16 on the GPU.
+        weight: [N, K] nn.Linear weight (read in place).
+        bias: optional [N].
+        act: None or "gelu" (erf GELU epilogue).
+    """
+    require_device(x, weight, *([bias] if bias is not None else []))
+    if act not in (None, "gelu"):
+        raise ValueError(f"unsupported activation {act!r}")
+    if not linear_eligible(x, weight, bias):
+        raise ValueError(f"linear_hip: unsupported shape x{tuple(x.shape)} w{tuple(weight.shape)}"
+                         f" (need K % {K_MULTIPLE} == 0 and N % {N_MULTIPLE} == 0)")
+    shape = x.shape
+    x2d = _gemm_ready(rows2d(x))
+    w = _gemm_ready(weight)
+    b = None if bias is None else bias.contiguous()
+    M, K = x2d.shape
+    N = w.shape[0]
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    with _lib.device_of(x):
+        _lib.call("umic_linear_bf16", x2d.data_ptr(), w.data_ptr(), _lib.ptr(b), out.data_ptr(),
+                  M, N, K, ld(x2d), ld(w), N,
+                  _lib.UMIC_ACT_GELU if act == "gelu" else _lib.UMIC_ACT_NONE,
+                  _lib.stream_of(x))
+    return out.reshape(*shape[:-1], N)
+
+
+# Name of the reference's wrapper (src/umic/kernels/linear.py:118).
+linear_triton = linear_hip

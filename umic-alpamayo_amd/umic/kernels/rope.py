@@ -1,0 +1,172 @@
+"""Fused rotary embedding of q and k on gfx950 (libumic_hip.so).
+
+Drop-in for the reference's RoPE wrappers (src/umic/kernels/rope.py):
+``apply_rotary_vision_hip`` replaces ``apply_rotary_vision_triton`` (:78-84,
+signature of HF ``apply_rotary_pos_emb_vision``) and ``make_text_rope`` (:86-107)
+builds the replacement for HF ``apply_rotary_pos_emb``.  Unlike the reference,
+q and k are rotated in ONE launch that reads cos/sin once.
+
+Numerics are the eager HF functions' own:
+  text    (modeling_qwen3_vl.py:412-435)  every op in bf16 --
+          bf16(bf16(q*cos) + bf16(rotate_half(q)*sin)), cos/sin bf16;
+  vision  (modeling_qwen3_vl.py:145-156)  q.float(), fp32 cos/sin, products
+          and sum each rounded in fp32, one final cast to bf16.
+Outputs are allocated like eager's: ``torch.empty_like`` keeps a dense input's
+strides (so a transposed [B,H,S,D] view of [B,S,H,D] stays in that layout)
+and gives a contiguous tensor for a strided view such as q/k of a packed qkv.
+"""
+
+from __future__ import annotations
+
+import inspect
+
+import torch
+
+from umic import _lib
+from umic.kernels._common import require_device
+
+
+def _strides_bsh(t: torch.Tensor, order: str) -> tuple[int, int, int]:
+    """(batch, position, head) element strides of t laid out as `order`."""
+    if order == "bhsd":
+        return t.stride(0), t.stride(2), t.stride(1)
+    if order == "shd":
+        return 0, t.stride(0), t.stride(1)
+    raise ValueError(order)
+
+
+def _rope(q, k, cos, sin, mode: int, order: str) -> tuple[torch.Tensor, torch.Tensor]:
+    if order == "bhsd":
+        B, Hq, S, D = q.shape
+        Hk = k.shape[1]
+        cs_sb = cos.stride(0) if cos.shape[0] == B else 0
+        cs_ss = cos.stride(1)
+    else:
+        S, Hq, D = q.shape
+        B, Hk = 1, k.shape[1]
+        cs_sb, cs_ss = 0, cos.stride(0)
+    q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+    qs, ks = _strides_bsh(q, order), _strides_bsh(k, order)
+    qos, kos = _strides_bsh(q_out, order), _strides_bsh(k_out, order)
+    with _lib.device_of(q):
+        _lib.call("umic_rope_qk_bf16", q.data_ptr(), k.data_ptr(), q_out.data_ptr(),
+                  k_out.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                  int(cos.dtype == torch.float32), mode, B, S, Hq, Hk, D,
+                  *qs, *ks, *qos, *kos, cs_sb, cs_ss, _lib.stream_of(q))
+    return q_out, k_out
+
+
+def _same_table_layout(cos: torch.Tensor, sin: torch.Tensor) -> bool:
+    return (cos.shape == sin.shape and cos.stride() == sin.stride() and cos.dtype == sin.dtype
+            and cos.device == sin.device and cos.stride(-1) == 1)
+
+
+def text_rope_eligible(q, k, cos, sin, unsqueeze_dim=1) -> bool:
+    """HF text layout the kernel reproduces exactly: q/k [B,H,S,D] bf16 on the
+    GPU, cos/sin [B or 1, S, D] bf16, broadcast over heads (unsqueeze_dim 1)."""
+    if unsqueeze_dim != 1 or not all(isinstance(t, torch.Tensor) for t in (q, k, cos, sin)):
+        return False
+    if not (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+            and cos.dtype == torch.bfloat16 and q.dim() == 4 and k.dim() == 4 and cos.dim() == 3):
+        return False
+    B, _, S, D = q.shape
+    return (k.shape[0] == B and k.shape[2] == S and k.shape[3] == D and D % 2 == 0
+            and cos.shape[1] == S and cos.shape[2] == D and cos.shape[0] in (1, B)
+            and q.stride(-1) == 1 and k.stride(-1) == 1 and _same_table_layout(cos, sin)
+            and k.device == q.device and cos.device == q.device)
+
+
+def vision_rope_eligible(q, k, cos, sin) -> bool:
+    """HF vision layout: q/k [S,H,D] bf16 on the GPU, cos/sin [S, D] fp32/bf16."""
+    if not all(isinstance(t, torch.Tensor) for t in (q, k, cos, sin)):
+        return False
+    if not (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+            and q.dim() == 3 and k.dim() == 3 and cos.dim() == 2
+            and cos.dtype in (torch.float32, torch.bfloat16)):
+        return False
+    S, _, D = q.shape
+    return (k.shape[0] == S and k.shape[2] == D and D % 2 == 0 and tuple(cos.shape) == (S, D)
+            and q.stride(-1) == 1 and k.stride(-1) == 1 and _same_table_layout(cos, sin)
+            and k.device == q.device and cos.device == q.device)
+
+
+def apply_rotary_text_hip(q, k, cos, sin):
+    """HF text RoPE (unsqueeze_dim=1): q [B,Hq,S,D], k [B,Hk,S,D], cos/sin [B,S,D]."""
+    require_device(q, k, cos, sin)
+    if not text_rope_eligible(q, k, cos, sin):
+        raise ValueError("apply_rotary_text_hip: unsupported layout "
+                         f"q{tuple(q.shape)} k{tuple(k.shape)} cos{tuple(cos.shape)}")
+    return _rope(q, k, cos, sin, _lib.UMIC_ROPE_TEXT, "bhsd")
+
+
+def apply_rotary_vision_hip(q, k, cos, sin):
+    """Drop-in for HF apply_rotary_pos_emb_vision (q/k: [S, H, D])."""
+    if not (q.is_cuda and cos.is_cuda):
+        raise ValueError("apply_rotary_vision_hip: GPU tensors required")
+    require_device(q, k)
+    if not vision_rope_eligible(q, k, cos, sin):
+        raise ValueError("apply_rotary_vision_hip: unsupported layout "
+                         f"q{tuple(q.shape)} k{tuple(k.shape)} cos{tuple(cos.shape)}")
+    return _rope(q, k, cos, sin, _lib.UMIC_ROPE_VISION, "shd")
+
+
+def _unsqueeze_dim_of(fallback):
+    """Return f(args, kwargs) -> unsqueeze_dim for calls of `fallback`'s signature.
+
+    transformers 5.x has apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=1);
+    4.x had a position_ids parameter before it.  Binding against the wrapped
+    function's own signature reads the argument correctly in both.
+    """
+    try:
+        sig = inspect.signature(fallback)
+    except (TypeError, ValueError):
+        sig = None
+
+    def get(args, kwargs):
+        if sig is None:
+            return kwargs.get("unsqueeze_dim", 1 if not args else None)
+        try:
+            bound = sig.bind(None, None, None, None, *args, **kwargs)
+        except TypeError:
+            return None
+        bound.apply_defaults()
+        return bound.arguments.get("unsqueeze_dim", 1)
+
+    return get
+
+
+def make_text_rope(fallback):
+    """Build a drop-in for HF apply_rotary_pos_emb around `fallback`.
+
+    The HF layout (q/k [B,H,S,D] bf16 on the GPU, cos/sin [B,S,D] bf16,
+    unsqueeze_dim 1) runs the fused kernel; every other call -- CPU tensors,
+    other dtypes or layouts -- goes to `fallback` with its arguments untouched.
+    Any batch size is handled (the reference's fast path required B == 1).
+    """
+    unsq = _unsqueeze_dim_of(fallback)
+
+    def apply_rotary_text(q, k, cos, sin, *args, **kwargs):
+        if text_rope_eligible(q, k, cos, sin, unsq(args, kwargs)):
+            require_device(q, k, cos, sin)
+            return _rope(q, k, cos, sin, _lib.UMIC_ROPE_TEXT, "bhsd")
+        return fallback(q, k, cos, sin, *args, **kwargs)
+
+    apply_rotary_text.__wrapped__ = fallback
+    return apply_rotary_text
+
+
+def make_vision_rope(fallback):
+    """Drop-in for HF apply_rotary_pos_emb_vision with an eager fallback."""
+
+    def apply_rotary_vision(q, k, cos, sin, *args, **kwargs):
+        if not args and not kwargs and vision_rope_eligible(q, k, cos, sin):
+            require_device(q, k)
+            return _rope(q, k, cos, sin, _lib.UMIC_ROPE_VISION, "shd")
+        return fallback(q, k, cos, sin, *args, **kwargs)
+
+    apply_rotary_vision.__wrapped__ = fallback
+    return apply_rotary_vision
+
+
+# Name of the reference's vision wrapper (src/umic/kernels/rope.py:78).
+apply_rotary_vision_triton = apply_rotary_vision_hip
