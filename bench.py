@@ -14,11 +14,15 @@ the BASELINE shapes, every kernel launched once through the C ABI:
   down_proj        [3100,12288] x [4096,12288]^T on the vendor BLAS (F.linear),
                    as in the reference; with P5 it makes the LM MLP prefill.
 
-Inputs are resident in HBM before timing.  The HBM-bound kernels rotate over
-NSETS input sets (> 1 GB in total) so consecutive steps cannot be served from
-the 256 MB Infinity Cache.  Per-kernel durations come from HIP events
-recorded on the stream the kernels are launched on (torch's current stream),
-around each launch; the step time from a synchronised wall clock.
+Inputs are resident in HBM before timing.  Each HBM-bound kernel rotates
+over its own ring of input sets (and keeps its outputs alive for one ring
+turn) sized so a set is revisited only after >= 640 MB of other traffic:
+nothing can be served from the 256 MB Infinity Cache.  Timing: the K launches
+of one kernel run back-to-back between two HIP events recorded on the stream
+they are launched on (torch's current stream); each group is preceded by an
+untimed spacer launch (two P5 GEMMs) so the host has queued the whole group
+before the first event fires and host launch latency never shows up as GPU
+time.  ms_per_step is the sum over kernels of the per-launch event time.
 
 Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
 six fused norm/RoPE kernels (algorithmic bytes / summed durations);
@@ -42,14 +46,14 @@ for _p in (ROOT, os.path.join(ROOT, "umic-alpamayo_amd")):
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-NSETS = 4
 METRIC = "fused-kernel HBM GB/s (% of peak) + LM MLP prefill ms at M=3100 bf16"
 
 
-def _bf(*shape, scale=1.0, shift=0.0, gen=None, device="cuda"):
+def _bf(*shape, scale=1.0, shift=0.0, gen=None):
+    """N(shift, scale^2) bf16 tensor drawn directly on the GPU."""
     import torch
 
-    return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16).to(device)
+    return (shift + scale * torch.randn(*shape, generator=gen, device="cuda")).to(torch.bfloat16)
 
 
 def build_workload():
@@ -63,7 +67,7 @@ def build_workload():
 
     from umic.kernels import fused_ffn, layernorm, linear, rmsnorm, rope
 
-    g = torch.Generator().manual_seed(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
     M, H = 3100, 4096
     MV, HV = 16384, 1280
     w_rms = _bf(H, scale=0.1, shift=1.0, gen=g)
@@ -87,16 +91,19 @@ def build_workload():
     vemb = torch.cat((vemb, vemb), -1)
     cos_v, sin_v = vemb.cos().cuda(), vemb.sin().cuda()
 
-    sets = []
-    for _ in range(NSETS):
-        s = {
-            "x": _bf(M, H, gen=g), "r": _bf(M, H, gen=g),
-            "xv": _bf(MV, HV, gen=g), "rv": _bf(MV, HV, gen=g),
-            "q": _bf(1, M, 32, D, gen=g).transpose(1, 2),
-            "k": _bf(1, M, 8, D, gen=g).transpose(1, 2),
-            "qkv": _bf(MV, 3, 16, 80, gen=g),
-        }
-        sets.append(s)
+    RING_BYTES = 640e6
+
+    def ring(nbytes, make):
+        n = max(2, min(16, int(-(-RING_BYTES // nbytes))))
+        return [make() for _ in range(n)]
+
+    rms_x = ring(4 * M * H, lambda: _bf(M, H, gen=g))
+    add_xr = ring(8 * M * H, lambda: (_bf(M, H, gen=g), _bf(M, H, gen=g)))
+    ln_x = ring(4 * MV * HV, lambda: _bf(MV, HV, gen=g))
+    addln_xr = ring(8 * MV * HV, lambda: (_bf(MV, HV, gen=g), _bf(MV, HV, gen=g)))
+    rope_qk = ring(4 * 40 * M * D, lambda: (_bf(1, M, 32, D, gen=g).transpose(1, 2),
+                                            _bf(1, M, 8, D, gen=g).transpose(1, 2)))
+    rope_qkv = ring(8 * 16 * MV * 80, lambda: _bf(MV, 3, 16, 80, gen=g))
 
     xg = _bf(M, H, gen=g)
     wq = _bf(H, H, scale=0.02, gen=g)
@@ -107,25 +114,25 @@ def build_workload():
     hmid = _bf(M, 12288, gen=g)
     eps = 1e-6
 
-    def S(i):
-        return sets[i % NSETS]
+    def pick(r, i):
+        return r[i % len(r)]
 
     def vision(i):
-        q, k, _ = S(i)["qkv"].permute(1, 0, 2, 3).unbind(0)
-        rope.apply_rotary_vision_hip(q, k, cos_v, sin_v)
+        q, k, _ = pick(rope_qkv, i).permute(1, 0, 2, 3).unbind(0)
+        return rope.apply_rotary_vision_hip(q, k, cos_v, sin_v)
 
     b2 = 2
     ents = [
-        ("rmsnorm", lambda i: rmsnorm.rmsnorm_hip(S(i)["x"], w_rms, eps),
+        ("rmsnorm", lambda i: rmsnorm.rmsnorm_hip(pick(rms_x, i), w_rms, eps),
          2 * M * H * b2 + H * b2, 0, "hbm"),
-        ("add_rmsnorm", lambda i: rmsnorm.add_rmsnorm_hip(S(i)["x"], S(i)["r"], w_rms, eps),
+        ("add_rmsnorm", lambda i: rmsnorm.add_rmsnorm_hip(*pick(add_xr, i), w_rms, eps),
          4 * M * H * b2 + H * b2, 0, "hbm"),
-        ("layernorm", lambda i: layernorm.layernorm_hip(S(i)["xv"], w_ln, b_ln, eps),
+        ("layernorm", lambda i: layernorm.layernorm_hip(pick(ln_x, i), w_ln, b_ln, eps),
          2 * MV * HV * b2 + 2 * HV * b2, 0, "hbm"),
-        ("add_layernorm", lambda i: layernorm.add_layernorm_hip(S(i)["xv"], S(i)["rv"], w_ln, b_ln,
+        ("add_layernorm", lambda i: layernorm.add_layernorm_hip(*pick(addln_xr, i), w_ln, b_ln,
                                                                 eps),
          4 * MV * HV * b2 + 2 * HV * b2, 0, "hbm"),
-        ("rope_text", lambda i: rope.apply_rotary_text_hip(S(i)["q"], S(i)["k"], cos_t, sin_t),
+        ("rope_text", lambda i: rope.apply_rotary_text_hip(*pick(rope_qk, i), cos_t, sin_t),
          2 * b2 * (32 + 8) * M * D + 2 * b2 * M * D, 0, "hbm"),
         ("rope_vision", vision, 2 * b2 * 2 * 16 * MV * 80 + 2 * 4 * MV * 80, 0, "hbm"),
         ("q_proj", lambda i: linear.linear_hip(xg, wq), (M * H + H * H + M * H) * b2,
@@ -137,7 +144,11 @@ def build_workload():
         ("down_proj", lambda i: torch.nn.functional.linear(hmid, wd),
          (M * 12288 + H * 12288 + M * H) * b2, 2 * M * H * 12288, "mfma"),
     ]
-    return ents
+    rings = {"rmsnorm": len(rms_x), "add_rmsnorm": len(add_xr), "layernorm": len(ln_x),
+             "add_layernorm": len(addln_xr), "rope_text": len(rope_qk),
+             "rope_vision": len(rope_qkv)}
+    spacer = lambda: fused_ffn.gate_silu_mul_hip(xg, wg.t(), wu.t())  # noqa: E731
+    return ents, rings, spacer
 
 
 def cpu_baseline(sample_s: float) -> dict:
@@ -199,6 +210,36 @@ def load_traffic(name: str):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+def pmc_probe() -> int:
+    """One launch of each kernel after a plain device copy of known size.
+
+    Run under ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``): the copy
+    reads and writes exactly COPY_BYTES, which calibrates the counters'
+    per-dispatch byte figures for the kernels that follow.
+    """
+    import torch
+
+    from umic import _lib
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    ents, _, _ = build_workload()
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    for name, fn, nbytes, *_ in [("copy", lambda i: dst.copy_(src), 2 * COPY_BYTES)] + ents:
+        flush.zero_()  # evict the Infinity Cache between probes
+        torch.cuda.synchronize()
+        fn(0)
+        torch.cuda.synchronize()
+        print(f"probe {name} algorithmic_bytes={nbytes}", flush=True)
+    return 0
+
+
+COPY_BYTES = 512 << 20
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +247,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-sample-s", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -213,13 +256,16 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.pmc_probe:
+        return pmc_probe()
+
     import torch
 
     from umic import _lib
 
     _lib.load()
     torch.cuda.set_device(0)
-    ents = build_workload()
+    ents, rings, spacer = build_workload()
     torch.cuda.synchronize()
 
     for i in range(args.warmup):
@@ -228,21 +274,25 @@ def main() -> int:
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in ents] for _ in range(K)]
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in ents]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(K):
-        for j, (_, fn, *_) in enumerate(ents):
-            ev[s][j][0].record()
-            fn(s)
-            ev[s][j][1].record()
+    for j, (name, fn, *_) in enumerate(ents):
+        keep = [None] * rings.get(name, 1)  # outputs live for one ring turn
+        spacer()
+        spacer()
+        evs[j][0].record()
+        for s in range(K):
+            keep[s % len(keep)] = fn(s)
+        evs[j][1].record()
+        del keep
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
     kern = {}
     for j, (name, _, nbytes, flops, bound) in enumerate(ents):
-        us = sum(ev[s][j][0].elapsed_time(ev[s][j][1]) for s in range(K)) / K * 1e3
+        us = evs[j][0].elapsed_time(evs[j][1]) / K * 1e3
         rec = {"us": round(us, 2), "bound": bound, "bytes": nbytes}
         rec["gbps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
         if bound == "hbm":
@@ -274,7 +324,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(wall / K * 1e3, 3),
+        "ms_per_step": round(sum(k["us"] for k in kern.values()) / 1e3, 3),
+        "wall_ms_per_step": round(wall / K * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -283,7 +334,7 @@ def main() -> int:
         "config": {"workload": "BASELINE configs 2-4 at full size: norms [3100,4096] and "
                                "[16384,1280], RoPE text q/k [1,32|8,3100,128] and vision "
                                "[16384,16,80], q/o proj and P5 MLP at M=3100 K=4096 N=4096|12288",
-                   "rows_lm": 3100, "rows_vit": 16384, "input_sets": NSETS},
+                   "rows_lm": 3100, "rows_vit": 16384, "input_rings": rings},
         "hbm_frac": round(agg / HBM_PEAK_GBS, 4),
         "mlp_prefill_ms": round(mlp_ms, 4),
         "kernels": kern,

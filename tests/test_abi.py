@@ -80,6 +80,13 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_rmsnorm_bf16(fake, fake, fake, -1, 64, 64, 64, 1e-6, None) == E_ARG
     assert lib.umic_rmsnorm_bf16(fake, fake, fake, 4, 64, 32, 64, 1e-6, None) == E_ARG
     assert lib.umic_rmsnorm_bf16(fake, fake, fake, 0, 64, 64, 64, 1e-6, None) == 0
+    # empty tensors carry null data pointers in torch: accepted, nothing launched
+    assert lib.umic_rmsnorm_bf16(None, None, None, 0, 64, 64, 64, 1e-6, None) == 0
+    assert lib.umic_add_layernorm_bf16(None, None, None, None, None, None, 0, 64, 64, 64, 64,
+                                       64, 1e-6, None) == 0
+    assert lib.umic_linear_bf16(None, None, None, None, 0, 64, 128, 128, 128, 64, 0, None) == 0
+    assert lib.umic_gate_silu_mul_bf16(None, None, None, None, 0, 64, 128, 128, 128, 128, 64,
+                                       None) == 0
     assert lib.umic_add_rmsnorm_bf16(fake, None, fake, fake, fake, 4, 64, 64, 64, 64, 64,
                                      1e-6, None) == E_ARG
     assert lib.umic_layernorm_bf16(fake, fake, None, fake, 4, 64, 64, 64, 1e-6, None) == E_ARG

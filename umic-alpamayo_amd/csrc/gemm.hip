@@ -37,11 +37,10 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kBM = 256;     // x rows per tile
-constexpr int kBW = 256;     // weight rows per tile (gate+up for P5)
-constexpr int kBK = 64;      // K per pipeline step
-constexpr int kChunks = kBK / 8;  // 16-byte chunks per LDS row
+constexpr int kBM = 256;  // x rows per tile
+constexpr int kBW = 256;  // weight rows per tile (gate+up for P5)
 
 struct GemmArgs {
   const uint16_t* x;
@@ -53,16 +52,51 @@ struct GemmArgs {
   int tiles_m, tiles;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ (row & 7)); }
+// LDS geometry for a K step of BK elements.  A tile row is BK bf16 = BK*2
+// bytes = CPR 16-byte chunks; one direct-to-LDS wave instruction moves
+// 64 x 16 B = 1 KB = RPI consecutive rows.  Chunks are XOR-swizzled within a
+// row so that the 8 lanes serviced together by a 128-byte LDS access (the
+// MFMA fragment reads walk 8 consecutive rows at a fixed chunk) land on 8
+// distinct 16-byte bank groups.
+template <int BK>
+struct Geo {
+  static constexpr int CPR = BK / 8;
+  static constexpr int RPI = 64 / CPR;
+  static __device__ __forceinline__ int swz(int row) {
+    if constexpr (BK == 64) return row & 7;          // 128 B rows
+    else return (row >> 1) & 3;                      // 64 B rows, 2 per 128 B
+  }
+  static __device__ __forceinline__ int slot(int row, int chunk) {
+    return row * CPR + (chunk ^ swz(row));
+  }
+};
 
-template <int NB, int ACT, bool BIAS>
+// Workgroup barrier for the LDS pipeline: wait until at most PENDING of this
+// wave's direct-to-LDS loads are still in flight (the older ones -- the next
+// stage -- have landed) and its LDS reads are done, then s_barrier.  Written
+// out (rather than __syncthreads, whose fence drains every load) so the
+// deeper stages stay in flight across the barrier; the asm is a compiler
+// memory barrier, so no LDS access moves across it.
+template <int PENDING>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(PENDING >= 0 && PENDING < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
+}
+
+template <int NB, int ACT, bool BIAS, int BK, int STAGES>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
-  // [stage][operand: 0 weights, 1 x][row][chunk] as 16-byte units (128 KB)
-  __shared__ u32x4 lds[2][2][kBM * kChunks];
+  using G = Geo<BK>;
+  constexpr int CPR = G::CPR, RPI = G::RPI;
+  constexpr int KK = BK / 16;                  // MFMA K slices per stage
+  constexpr int L = 2 * (64 / RPI);            // DMA instructions per wave per stage
+  // [stage][operand: 0 weights, 1 x][row * CPR + slot], 16-byte units
+  __shared__ u32x4 lds[STAGES][2][kBM * CPR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform (scalar) wave index: the operand pointers chosen from it
+  // must live in SGPRs for the buffer resources
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
   // XCD-aware remap: physical ids b, b+8, b+16, ... (one XCD) take
@@ -72,35 +106,40 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   if (logical >= g.tiles) return;
   const int tm = logical % g.tiles_m;
   const int tn = logical / g.tiles_m;
-  const int64_t m0 = (int64_t)tm * kBM;
-  const int64_t n0 = (int64_t)tn * (NB == 1 ? kBW : kBW / 2);
+  const int m0 = tm * kBM;
+  const int n0 = tn * (NB == 1 ? kBW : kBW / 2);
 
-  // This thread's 8 weight chunks and 8 x chunks per K step: tile row
-  // i*32 + tid/8, chunk tid%8.  Rows past the matrix edge re-read the last
-  // row (in bounds); their results are never stored.
-  const int crow = tid >> 3, cchunk = tid & 7;
-  const uint16_t* wsrc[8];
-  const uint16_t* xsrc[8];
+  // Buffer resources: rows past M / N read as zero (hardware range check),
+  // so ragged edge tiles need no clamping or predication in the K loop.
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(g.M * g.ldx * 2), 0x00020000);
+  const uint16_t* wsrc = (NB == 2 && wave >= 2) ? g.w1 : g.w0;
+  const int64_t ldw = (NB == 2 && wave >= 2) ? g.ldw1 : g.ldw0;
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wsrc, (short)0, (int)(g.N * ldw * 2), 0x00020000);
+
+  // This wave DMAs tile rows [wave*64, wave*64+64) of both operands.  Lane
+  // l writes LDS slot l % CPR of row l / CPR of each 1 KB group, so it
+  // fetches the chunk that the swizzle places there.
+  const int lr = lane / CPR;
+  const int lchunk = (lane % CPR) ^ G::swz(lr);
+  const int wrow0 = NB == 1 ? n0 + wave * 64 : n0 + (wave & 1) * 64;
+  const int xrow0 = m0 + wave * 64;
+  const int woff = (int)(((int64_t)(wrow0 + lr) * ldw + lchunk * 8) * 2);
+  const int xoff = (int)(((int64_t)(xrow0 + lr) * g.ldx + lchunk * 8) * 2);
+  const int wstep = (int)(RPI * ldw * 2), xstep = (int)(RPI * g.ldx * 2);
+
+  auto issue = [&](int stage, int k0) {
+    lds_void* dw = (lds_void*)&lds[stage][0][wave * 64 * CPR];
+    lds_void* dx = (lds_void*)&lds[stage][1][wave * 64 * CPR];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = i * 32 + crow;
-    int64_t wr;
-    const uint16_t* wb;
-    int64_t ldw;
-    if (NB == 1 || r < kBW / 2) {
-      wr = n0 + r;
-      wb = g.w0;
-      ldw = g.ldw0;
-    } else {
-      wr = n0 + r - kBW / 2;
-      wb = g.w1;
-      ldw = g.ldw1;
+    for (int j = 0; j < 64 / RPI; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)((__attribute__((address_space(3))) char*)dw + j * 1024),
+                                               16, woff + j * wstep + k0 * 2, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)((__attribute__((address_space(3))) char*)dx + j * 1024),
+                                               16, xoff + j * xstep + k0 * 2, 0, 0, 0);
     }
-    wr = wr < g.N ? wr : g.N - 1;
-    const int64_t xr = (m0 + r) < g.M ? (m0 + r) : g.M - 1;
-    wsrc[i] = wb + wr * ldw + cchunk * 8;
-    xsrc[i] = g.x + xr * g.ldx + cchunk * 8;
-  }
+  };
 
   // Fragment rows: a-blocks (weights) and b-blocks (x), 32 rows each.
   int arow[4], brow[4];
@@ -120,48 +159,51 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  u32x4 wst[8], xst[8];
-  auto fetch = [&](int64_t k0) {
+  bf16x8_t fa[2][4], fb[2][4];
+  auto frags = [&](int buf, int stage, int kk) {
+    const int ch = kk * 2 + fk;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      wst[i] = *reinterpret_cast<const u32x4*>(wsrc[i] + k0);
-      xst[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + k0);
+    for (int a = 0; a < 4; ++a) {
+      fa[buf][a] = __builtin_bit_cast(bf16x8_t, lds[stage][0][G::slot(arow[a] + frow, ch)]);
+      fb[buf][a] = __builtin_bit_cast(bf16x8_t, lds[stage][1][G::slot(brow[a] + frow, ch)]);
     }
   };
-  auto stash = [&](int s) {
+  auto mma = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = i * 32 + crow;
-      lds[s][0][swz(r, cchunk)] = wst[i];
-      lds[s][1][swz(r, cchunk)] = xst[i];
-    }
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][a], fb[buf][b], acc[a][b], 0, 0, 0);
   };
 
-  const int ksteps = (int)(g.K / kBK);
-  fetch(0);
-  stash(0);
-  __syncthreads();
+  const int KT = (int)(g.K / BK);
+  // Prologue: STAGES-1 K steps in flight, wait for the first.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) issue(s, s * BK);
+  if (KT >= STAGES - 1) stage_barrier<(STAGES - 2) * L>();
+  else stage_barrier<0>();
+  frags(0, 0, 0);
 
-  for (int kt = 0; kt < ksteps; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < ksteps) fetch((int64_t)(kt + 1) * kBK);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int st = kt % STAGES;
+    // Refill the buffer consumed in the previous step (all waves are past
+    // the barrier that ended their reads of it).
+    if (kt + STAGES - 1 < KT) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      bf16x8_t af[4], bfr[4];
-      const int ch = kk * 2 + fk;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        af[a] = __builtin_bit_cast(bf16x8_t, lds[s][0][swz(arow[a] + frow, ch)]);
-        bfr[a] = __builtin_bit_cast(bf16x8_t, lds[s][1][swz(brow[a] + frow, ch)]);
+    for (int kk = 0; kk < KK; ++kk) {
+      const int cur = kk & 1;
+      if (kk < KK - 1) {
+        frags(cur ^ 1, st, kk + 1);
+      } else {
+        // Step kt+1's tile must have landed (loads issued after it may stay
+        // in flight), then everyone may start reading it.
+        if (kt + STAGES - 1 < KT) stage_barrier<(STAGES - 2) * L>();
+        else stage_barrier<0>();
+        if (kt + 1 < KT) frags(cur ^ 1, (kt + 1) % STAGES, 0);
       }
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+      mma(cur);
     }
-    if (kt + 1 < ksteps) stash(s ^ 1);
-    __syncthreads();
   }
 
   // Epilogue.  acc[a][b][r]: weight row 8*(r/4) + 4*(lane/32) + r%4 of
@@ -169,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   constexpr int kOutBlocks = NB == 1 ? 4 : 2;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    const int64_t m = m0 + brow[b] + frow;
+    const int64_t m = (int64_t)m0 + brow[b] + frow;
     if (m >= g.M) continue;
     uint16_t* orow = g.out + m * g.ldo;
 #pragma unroll
@@ -200,6 +242,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   }
 }
 
+constexpr int kBK = 64;
+constexpr int kStages = 2;
+
 template <int NB, int ACT, bool BIAS>
 int launch_gemm(GemmArgs g, hipStream_t st) {
   const int64_t bn = NB == 1 ? kBW : kBW / 2;
@@ -209,15 +254,21 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
   g.tiles_m = (int)tm;
   g.tiles = (int)(tm * tn);
   const int64_t grid = ((g.tiles + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS>), dim3((unsigned)grid), dim3(256), 0, st, g);
+  hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS, kBK, kStages>), dim3((unsigned)grid), dim3(256), 0,
+                     st, g);
   return launch_status();
 }
 
+// Buffer-resource offsets are 32-bit: every operand (rows x leading dim)
+// must stay below 2 GiB, and tile row offsets below 2^31 as well.
 bool gemm_shape_ok(const void* x, const void* w0, const void* w1, const void* out, int64_t M,
                    int64_t N, int64_t K, int64_t ldx, int64_t ldw0, int64_t ldw1, int64_t ldo) {
   if (K % kBK != 0 || N % 8 != 0) return false;
   if (ldx % 8 || ldw0 % 8 || ldw1 % 8 || ldo % 8) return false;
   if (!aligned16(x) || !aligned16(w0) || !aligned16(w1) || !aligned16(out)) return false;
+  const int64_t lim = (int64_t)1 << 30;  // elements (2 GiB of bf16)
+  const int64_t mpad = (M + kBM - 1) / kBM * kBM, npad = (N + kBW - 1) / kBW * kBW;
+  if (mpad * ldx >= lim || npad * ldw0 >= lim || npad * ldw1 >= lim) return false;
   return true;
 }
 
@@ -229,10 +280,11 @@ using namespace umic;
 extern "C" int umic_linear_bf16(const void* x, const void* w, const void* bias, void* out,
                                 int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                                 int64_t ldo, int act, void* stream) {
-  if (!x || !w || !out || M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
+  if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
   if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU) return UMIC_ERR_INVALID_ARG;
-  if (M > 0 && N > 0 && (ldx < K || ldw < K || ldo < N)) return UMIC_ERR_INVALID_ARG;
-  if (M == 0 || N == 0) return UMIC_OK;
+  if (M == 0 || N == 0) return UMIC_OK;  // empty tensors may carry null pointers
+  if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
   if (K == 0) return UMIC_ERR_UNSUPPORTED;
   if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
   if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
@@ -247,9 +299,10 @@ extern "C" int umic_linear_bf16(const void* x, const void* w, const void* bias, 
 extern "C" int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void* wu, void* out,
                                        int64_t M, int64_t N, int64_t K, int64_t ldx,
                                        int64_t ldwg, int64_t ldwu, int64_t ldo, void* stream) {
-  if (!x || !wg || !wu || !out || M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
-  if (M > 0 && N > 0 && (ldx < K || ldwg < K || ldwu < K || ldo < N)) return UMIC_ERR_INVALID_ARG;
-  if (M == 0 || N == 0) return UMIC_OK;
+  if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return UMIC_OK;  // empty tensors may carry null pointers
+  if (!x || !wg || !wu || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldwg < K || ldwu < K || ldo < N) return UMIC_ERR_INVALID_ARG;
   if (K == 0) return UMIC_ERR_UNSUPPORTED;
   if (!gemm_shape_ok(x, wg, wu, out, M, N, K, ldx, ldwg, ldwu, ldo)) return UMIC_ERR_UNSUPPORTED;
   GemmArgs g{(const uint16_t*)x, (const uint16_t*)wg, (const uint16_t*)wu, nullptr,

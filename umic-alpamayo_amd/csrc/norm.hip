@@ -53,45 +53,60 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, in
   if (row >= a.rows) return;
 
   // The row's source values stay packed as bf16 (16 B per 8 elements) in
-  // registers between the statistics pass and the output pass.
+  // registers between the statistics pass and the output pass.  Loads are
+  // issued unconditionally (a dead slot re-reads vector 0 and is zeroed by a
+  // select): predicated loads would sit in branches, and every branch join
+  // costs a full vmcnt drain -- the loads must all be in flight together.
   const u32x4* xp = reinterpret_cast<const u32x4*>(a.x + row * a.ldx);
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  bool live[MAXV];
+  int cix[MAXV];
   u32x4 sv[MAXV];
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int c = i * LPR + lane;
-    if (i < vpl && c < nvec) sv[i] = ld_stream(xp + c);
-    else sv[i] = u32x4{0u, 0u, 0u, 0u};
+    live[i] = i < vpl && c < nvec;
+    cix[i] = live[i] ? c : 0;
+    sv[i] = ld_stream(xp + cix[i]);
   }
   if constexpr (has_add(OP)) {
     const u32x4* rp = reinterpret_cast<const u32x4*>(a.r + row * a.ldr);
-    u32x4* sp = reinterpret_cast<u32x4*>(a.s + row * a.lds);
+    u32x4 rv[MAXV];
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) rv[i] = ld_stream(rp + cix[i]);
 #pragma unroll
     for (int i = 0; i < MAXV; ++i) {
-      const int c = i * LPR + lane;
-      if (i < vpl && c < nvec) {
-        float xf[8], rf[8];
-        unpack8(sv[i], xf);
-        unpack8(ld_stream(rp + c), rf);
+      float xf[8], rf[8];
+      unpack8(sv[i], xf);
+      unpack8(rv[i], rf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[e] = xf[e] + rf[e];
-        sv[i] = pack8(xf);  // bf16(x + r): the eager residual add
-        st_stream(sp + c, sv[i]);
-      }
+      for (int e = 0; e < 8; ++e) xf[e] = xf[e] + rf[e];
+      sv[i] = pack8(xf);  // bf16(x + r): the eager residual add
     }
+    u32x4* sp = reinterpret_cast<u32x4*>(a.s + row * a.lds);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i)
+      if (live[i]) st_stream(sp + cix[i], sv[i]);
   }
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) sv[i] = live[i] ? sv[i] : zero;
 
-  // Exact double sums (zero-filled tail vectors contribute nothing).
-  double sum = 0.0, ssq = 0.0;
+  // Exact double sums (zero-filled tail vectors contribute nothing).  Four
+  // independent accumulators keep the f64 add chains short; the sums are
+  // exact, so the grouping does not change them.
+  double sum4[4] = {0.0, 0.0, 0.0, 0.0}, ssq4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     float f[8];
     unpack8(sv[i], f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if constexpr (is_ln(OP)) sum += (double)f[e];
-      ssq += (double)(f[e] * f[e]);  // a bf16 square is exact in fp32
+      if constexpr (is_ln(OP)) sum4[e & 3] += (double)f[e];
+      ssq4[e & 3] += (double)(f[e] * f[e]);  // a bf16 square is exact in fp32
     }
   }
+  double sum = (sum4[0] + sum4[1]) + (sum4[2] + sum4[3]);
+  double ssq = (ssq4[0] + ssq4[1]) + (ssq4[2] + ssq4[3]);
   const double inv_n = 1.0 / (double)a.n;
   float rstd, mean = 0.f;
   if constexpr (is_ln(OP)) {
@@ -107,16 +122,22 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, in
   const u32x4* wp = reinterpret_cast<const u32x4*>(a.w);
   const u32x4* bp = reinterpret_cast<const u32x4*>(a.b);
   u32x4* yp = reinterpret_cast<u32x4*>(a.y + row * a.ldy);
+  u32x4 wv[MAXV], bv[MAXV];
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
-    const int c = i * LPR + lane;
-    if (!(i < vpl && c < nvec)) continue;
+    wv[i] = wp[cix[i]];
+    if constexpr (is_ln(OP)) bv[i] = bp[cix[i]];
+  }
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    if (!live[i]) continue;
+    const int c = cix[i];
     float f[8], wf[8], o[8];
     unpack8(sv[i], f);
-    unpack8(wp[c], wf);
+    unpack8(wv[i], wf);
     if constexpr (is_ln(OP)) {
       float bf[8];
-      unpack8(bp[c], bf);
+      unpack8(bv[i], bf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wf[e], rstd * (f[e] - mean), bf[e]);
     } else {
@@ -198,11 +219,21 @@ int launch_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
 
 template <int OP, int LPR>
 int launch_lpr(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
-  if (vpl <= 1) return launch_rows<OP, LPR, 1>(a, nvec, vpl, st);
-  if (vpl <= 2) return launch_rows<OP, LPR, 2>(a, nvec, vpl, st);
-  if (vpl <= 4) return launch_rows<OP, LPR, 4>(a, nvec, vpl, st);
-  if (vpl <= 8) return launch_rows<OP, LPR, 8>(a, nvec, vpl, st);
-  return launch_rows<OP, LPR, 16>(a, nvec, vpl, st);
+  switch (vpl) {
+    case 1: return launch_rows<OP, LPR, 1>(a, nvec, vpl, st);
+    case 2: return launch_rows<OP, LPR, 2>(a, nvec, vpl, st);
+    case 3: return launch_rows<OP, LPR, 3>(a, nvec, vpl, st);
+    case 4: return launch_rows<OP, LPR, 4>(a, nvec, vpl, st);
+    case 5: return launch_rows<OP, LPR, 5>(a, nvec, vpl, st);
+    case 6: return launch_rows<OP, LPR, 6>(a, nvec, vpl, st);
+    case 7:
+    case 8: return launch_rows<OP, LPR, 8>(a, nvec, vpl, st);
+    case 9:
+    case 10: return launch_rows<OP, LPR, 10>(a, nvec, vpl, st);
+    case 11:
+    case 12: return launch_rows<OP, LPR, 12>(a, nvec, vpl, st);
+    default: return launch_rows<OP, LPR, 16>(a, nvec, vpl, st);
+  }
 }
 
 template <int OP>
@@ -239,12 +270,13 @@ int launch_norm(const NormArgs& a, hipStream_t st) {
 
 template <int OP>
 int norm_entry(NormArgs a, void* stream) {
-  if (!a.x || !a.w || !a.y || a.rows < 0 || a.n <= 0) return UMIC_ERR_INVALID_ARG;
+  if (a.rows < 0 || a.n <= 0) return UMIC_ERR_INVALID_ARG;
+  if (a.rows == 0) return UMIC_OK;  // empty tensors may carry null pointers
+  if (!a.x || !a.w || !a.y) return UMIC_ERR_INVALID_ARG;
   if (has_add(OP) && (!a.r || !a.s)) return UMIC_ERR_INVALID_ARG;
   if (is_ln(OP) && !a.b) return UMIC_ERR_INVALID_ARG;
   if (a.ldx < a.n || a.ldy < a.n) return UMIC_ERR_INVALID_ARG;
   if (has_add(OP) && (a.ldr < a.n || a.lds < a.n)) return UMIC_ERR_INVALID_ARG;
-  if (a.rows == 0) return UMIC_OK;
   return launch_norm<OP>(a, as_stream(stream));
 }
 

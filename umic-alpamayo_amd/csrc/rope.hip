@@ -40,6 +40,7 @@ struct RopeArgs {
 };
 
 constexpr int kMaxCsFloats = 4096;  // LDS budget per table (cos, sin): 16 KB each
+constexpr int kItems = 4;           // work items per thread per pass
 
 template <int VEC>
 struct Chunk;
@@ -97,66 +98,94 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int P) {
   const int D = (int)a.D;
   const int half = D / 2;
 
+  const int C = half / VEC;  // chunks per half row
+  const int ipp = (int)(a.Hq + a.Hk) * C;
+  const int nq = (int)a.Hq * C;
+  const int nitems = P * ipp;
   // Stage cos/sin rows of this block's positions (fp32 in LDS; bf16 widens
-  // exactly, so TEXT mode still multiplies by the bf16 values).
-  for (int i = threadIdx.x; i < P * D; i += blockDim.x) {
-    const int pp = i / D, d = i - pp * D;
-    const int64_t p = p0 + pp;
-    float c = 0.f, s = 0.f;
-    if (p < npos) {
+  // exactly, so TEXT mode still multiplies by the bf16 values).  Run after
+  // the first pass's q/k loads are in flight, so both latencies overlap.
+  auto stage_tables = [&]() {
+    for (int i = threadIdx.x; i < P * D; i += blockDim.x) {
+      const int pp = i / D, d = i - pp * D;
+      const int64_t p = p0 + pp;
+      float c = 0.f, s = 0.f;
+      if (p < npos) {
+        int64_t b = 0, sidx = p;
+        if (a.B != 1) {
+          b = p / a.S;
+          sidx = p - b * a.S;
+        }
+        const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+        if constexpr (CS32) {
+          c = static_cast<const float*>(a.cos)[off];
+          s = static_cast<const float*>(a.sin)[off];
+        } else {
+          c = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+          s = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+        }
+      }
+      cs_l[i] = c;
+      sn_l[i] = s;
+    }
+  };
+
+  // Each thread takes kItems items per pass; all their loads are issued
+  // before any is consumed (an item past the end re-reads item 0 of the
+  // block, always valid, and stores nothing).
+  for (int base = 0; base < nitems; base += kItems * 256) {
+    const uint16_t* xs[kItems];
+    uint16_t* os[kItems];
+    int cofs[kItems], dls[kItems];
+    bool ok[kItems];
+#pragma unroll
+    for (int u = 0; u < kItems; ++u) {
+      int it = base + u * 256 + (int)threadIdx.x;
+      const int pp0 = it / ipp;
+      ok[u] = it < nitems && p0 + pp0 < npos;
+      if (!ok[u]) it = 0;
+      const int pp = it / ipp;
+      const int j = it - pp * ipp;
+      const int64_t p = p0 + pp;
       int64_t b = 0, sidx = p;
       if (a.B != 1) {
         b = p / a.S;
         sidx = p - b * a.S;
       }
-      const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
-      if constexpr (CS32) {
-        c = static_cast<const float*>(a.cos)[off];
-        s = static_cast<const float*>(a.sin)[off];
+      const bool isq = j < nq;
+      const int jj = isq ? j : j - nq;
+      const int h = jj / C, c = jj - h * C;
+      if (isq) {
+        xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
+        os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
       } else {
-        c = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
-        s = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+        xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
+        os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
       }
+      dls[u] = c * VEC;
+      cofs[u] = pp * D;
     }
-    cs_l[i] = c;
-    sn_l[i] = s;
-  }
-  __syncthreads();
-
-  const int C = half / VEC;  // chunks per half row
-  const int ipp = (int)(a.Hq + a.Hk) * C;
-  const int nq = (int)a.Hq * C;
-  for (int it = threadIdx.x; it < P * ipp; it += blockDim.x) {
-    const int pp = it / ipp;
-    const int j = it - pp * ipp;
-    const int64_t p = p0 + pp;
-    if (p >= npos) break;  // items are position-major: the rest are out too
-    int64_t b = 0, sidx = p;
-    if (a.B != 1) {
-      b = p / a.S;
-      sidx = p - b * a.S;
+    float xl[kItems][VEC], xh[kItems][VEC];
+#pragma unroll
+    for (int u = 0; u < kItems; ++u) {
+      Chunk<VEC>::load(xs[u] + dls[u], xl[u]);
+      Chunk<VEC>::load(xs[u] + half + dls[u], xh[u]);
     }
-    const bool isq = j < nq;
-    const int jj = isq ? j : j - nq;
-    const int h = jj / C, c = jj - h * C;
-    const uint16_t* x;
-    uint16_t* o;
-    if (isq) {
-      x = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
-      o = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
-    } else {
-      x = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
-      o = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
+    if (base == 0) {  // uniform: every thread takes the first pass
+      stage_tables();
+      __syncthreads();
     }
-    const int dl = c * VEC, dh = half + c * VEC;
-    float xl[VEC], xh[VEC], ol[VEC], oh[VEC];
-    Chunk<VEC>::load(x + dl, xl);
-    Chunk<VEC>::load(x + dh, xh);
-    const float* cb = cs_l + pp * D;
-    const float* sb = sn_l + pp * D;
-    rotate<MODE, VEC>(xl, xh, cb + dl, cb + dh, sb + dl, sb + dh, ol, oh);
-    Chunk<VEC>::store(o + dl, ol);
-    Chunk<VEC>::store(o + dh, oh);
+#pragma unroll
+    for (int u = 0; u < kItems; ++u) {
+      if (!ok[u]) continue;
+      float ol[VEC], oh[VEC];
+      const float* cb = cs_l + cofs[u];
+      const float* sb = sn_l + cofs[u];
+      const int dl = dls[u], dh = half + dls[u];
+      rotate<MODE, VEC>(xl[u], xh[u], cb + dl, cb + dh, sb + dl, sb + dh, ol, oh);
+      Chunk<VEC>::store(os[u] + dl, ol);
+      Chunk<VEC>::store(os[u] + dh, oh);
+    }
   }
 }
 
@@ -164,8 +193,8 @@ template <int MODE, bool CS32, int VEC>
 int launch_rope(const RopeArgs& a, hipStream_t st) {
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
-  // ~1280 items per block (5 per thread), bounded by the LDS tables.
-  int64_t P = (1280 + ipp - 1) / ipp;
+  // About kItems items per thread (one pass), bounded by the LDS tables.
+  int64_t P = (kItems * 256 + ipp - 1) / ipp;
   if (P < 1) P = 1;
   if (P * a.D > kMaxCsFloats) P = kMaxCsFloats / a.D;
   const int64_t blocks = (npos + P - 1) / P;
@@ -196,13 +225,13 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
                                  int64_t cs_sb, int64_t cs_ss, void* stream) {
   if (mode != UMIC_ROPE_TEXT && mode != UMIC_ROPE_VISION) return UMIC_ERR_INVALID_ARG;
   if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
-  if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
-  if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
-  if (Hk > 0 && (!k || !k_out)) return UMIC_ERR_INVALID_ARG;
   if (mode == UMIC_ROPE_TEXT && cs_fp32) return UMIC_ERR_UNSUPPORTED;
   if (D % 2 != 0 || D > kMaxCsFloats) return UMIC_ERR_UNSUPPORTED;
   if ((Hq + Hk) * (D / 2) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
-  if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;
+  if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;  // empty: pointers may be null
+  if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
+  if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
+  if (Hk > 0 && (!k || !k_out)) return UMIC_ERR_INVALID_ARG;
 
   RopeArgs a{(const uint16_t*)q, (const uint16_t*)k, (uint16_t*)q_out, (uint16_t*)k_out,
              cos, sin, B, S, Hq, Hk, D,
