@@ -240,6 +240,32 @@ def pmc_probe() -> int:
 COPY_BYTES = 512 << 20
 
 
+def copy_ceiling() -> int:
+    """Practical HBM ceiling at the norm/RoPE sizes: torch's own device copy
+    (read n, write n) of the same byte counts, back-to-back over 12 buffers."""
+    import torch
+
+    torch.cuda.set_device(0)
+    for moved in (50_798_592, 83_891_200, 167_777_280, 400_000_000):
+        n = moved // 4  # bf16 elements per side
+        src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(12)]
+        dst = [torch.empty_like(src[0]) for _ in range(12)]
+        for i in range(12):
+            dst[i].copy_(src[i])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(12):
+            dst[i].copy_(src[i])
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 12 * 1e3
+        print(json.dumps({"copy_bytes_moved": moved, "us": round(us, 2),
+                          "gbps": round(moved / us / 1e3, 1)}), flush=True)
+        del src, dst
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +275,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="time plain device copies of the norm/RoPE byte counts")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -258,6 +286,8 @@ def main() -> int:
 
     if args.pmc_probe:
         return pmc_probe()
+    if args.copy_ceiling:
+        return copy_ceiling()
 
     import torch
 

@@ -27,9 +27,8 @@
 //
 // Workgroup order.  Hardware hands consecutive workgroup ids to the 8 XCDs
 // round-robin; the id is remapped so every XCD works through a contiguous
-// run of the m-fastest tile order, i.e. the workgroups sharing a weight tile
-// run on the same XCD at the same time and the weights stream from HBM
-// about once (x is small and stays L2/MALL resident).
+// run of a grouped tile order (4 tile rows at a time, m fastest), so the
+// tiles one XCD runs together share x and weight slabs in its 4 MB L2.
 #include "common.hpp"
 
 namespace umic {
@@ -39,8 +38,9 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kBM = 256;  // x rows per tile
-constexpr int kBW = 256;  // weight rows per tile (gate+up for P5)
+constexpr int kBM = 256;     // x rows per tile
+constexpr int kBW = 256;     // weight rows per tile (gate+up for P5)
+constexpr int kGroupM = 4;   // tile rows per L2 locality group
 
 struct GemmArgs {
   const uint16_t* x;
@@ -100,12 +100,19 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   const int wm = wave & 1, wn = wave >> 1;
 
   // XCD-aware remap: physical ids b, b+8, b+16, ... (one XCD) take
-  // consecutive logical tiles.
+  // consecutive logical tiles; logical tiles run in groups of kGroupM tile
+  // rows, m fastest inside a group, so the ~32 tiles an XCD holds at once
+  // form a kGroupM x 8 block whose x and weight slabs its L2 shares.
   const int per_xcd = (g.tiles + 7) >> 3;
   const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
   if (logical >= g.tiles) return;
-  const int tm = logical % g.tiles_m;
-  const int tn = logical / g.tiles_m;
+  const int tiles_n = g.tiles / g.tiles_m;
+  const int group = logical / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int gm = min(g.tiles_m - first_m, kGroupM);
+  const int in_group = logical - group * kGroupM * tiles_n;
+  const int tm = first_m + in_group % gm;
+  const int tn = in_group / gm;
   const int m0 = tm * kBM;
   const int n0 = tn * (NB == 1 ? kBW : kBW / 2);
 
@@ -225,8 +232,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 4; ++e) {
           float v = acc[a][b][rr * 4 + e];
           if constexpr (NB == 2) {
+            // silu(g) * u with the hardware exp2 / reciprocal (~1 ulp each,
+            // far inside the bf16 output rounding); large |g| saturates
+            // correctly: exp -> inf gives rcp -> 0, exp -> 0 gives rcp -> 1.
             const float u = acc[a + 2][b][rr * 4 + e];
-            v = v / (1.0f + __expf(-v)) * u;
+            const float den = 1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+            v = v * __builtin_amdgcn_rcpf(den) * u;
           } else {
             if constexpr (BIAS) v = v + bf2f(g.bias[n + e]);
             if constexpr (ACT == UMIC_ACT_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));

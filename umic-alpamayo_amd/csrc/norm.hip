@@ -45,9 +45,9 @@ struct NormArgs {
 
 template <int OP, int LPR, int MAXV>
 __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, int vpl) {
-  constexpr int kRowsPerBlock = 256 / LPR;
+  const int rows_per_block = (int)blockDim.x / LPR;
   const int lane = threadIdx.x & (LPR - 1);
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LPR;
+  const int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / LPR;
   // All LPR lanes of a group share `row`, so a group exits as a whole and
   // the butterflies below only ever read lanes of a live group.
   if (row >= a.rows) return;
@@ -208,12 +208,18 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(NormArgs a) {
 
 // ---- host dispatch --------------------------------------------------------
 
+// Block size: the hardware spreads workgroups evenly over the 256 CUs only
+// when there are many of them, so small row counts get 64- or 128-thread
+// blocks (the largest block that still yields >= 8 blocks per CU).
 template <int OP, int LPR, int MAXV>
 int launch_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
-  constexpr int kRowsPerBlock = 256 / LPR;
-  const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL((norm_rows_kernel<OP, LPR, MAXV>), dim3((unsigned)blocks), dim3(256), 0, st,
-                     a, nvec, vpl);
+  int threads = 256;
+  while (threads > 64 && (a.rows * LPR + threads - 1) / threads < 8 * 256) threads >>= 1;
+  const int rows_per_block = threads / LPR;
+  const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((norm_rows_kernel<OP, LPR, MAXV>), dim3((unsigned)blocks), dim3(threads), 0,
+                     st, a, nvec, vpl);
   return launch_status();
 }
 

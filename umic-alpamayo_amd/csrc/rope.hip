@@ -49,8 +49,11 @@ struct Chunk<8> {
   static __device__ __forceinline__ void load(const uint16_t* p, float f[8]) {
     unpack8(ld_stream(reinterpret_cast<const u32x4*>(p)), f);
   }
+  // Plain (cached) stores: a head row's two halves are written by two store
+  // instructions, and with D/2 not a multiple of 64 elements they share
+  // 128-byte lines, which L2 must merge before writing back.
   static __device__ __forceinline__ void store(uint16_t* p, const float f[8]) {
-    st_stream(reinterpret_cast<u32x4*>(p), pack8(f));
+    *reinterpret_cast<u32x4*>(p) = pack8(f);
   }
 };
 template <>
@@ -193,8 +196,9 @@ template <int MODE, bool CS32, int VEC>
 int launch_rope(const RopeArgs& a, hipStream_t st) {
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
-  // About kItems items per thread (one pass), bounded by the LDS tables.
-  int64_t P = (kItems * 256 + ipp - 1) / ipp;
+  // As many whole positions as fit kItems items per thread (one pass for
+  // the usual head counts), bounded by the LDS tables.
+  int64_t P = (kItems * 256) / ipp;
   if (P < 1) P = 1;
   if (P * a.D > kMaxCsFloats) P = kMaxCsFloats / a.D;
   const int64_t blocks = (npos + P - 1) / P;
