@@ -83,7 +83,12 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
 }
 
-template <int NB, int ACT, bool BIAS, int BK, int STAGES>
+// SCHED selects how the MFMA stream is interleaved with LDS reads and the
+// direct-to-LDS loads inside a K step: 0 leaves it to the compiler, 1 and 2
+// are the compiler's built-in GEMM strategies (iglp_opt 0 / 1), 3 pins one
+// LDS read (and on the first slice one load) after each of the first MFMAs
+// and fences each K slice, 4 only fences each K slice.
+template <int NB, int ACT, bool BIAS, int BK, int STAGES, int SCHED>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   using G = Geo<BK>;
   constexpr int CPR = G::CPR, RPI = G::RPI;
@@ -192,26 +197,50 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   else stage_barrier<0>();
   frags(0, 0, 0);
 
+  // The loop body is branch-free (one basic block the scheduler can
+  // interleave): the last STAGES-1 steps still refill a buffer that is never
+  // read again, from offsets past K -- in-range garbage or range-checked
+  // zeros -- and the last step reads next-stage fragments it never uses.
   for (int kt = 0; kt < KT; ++kt) {
     const int st = kt % STAGES;
     // Refill the buffer consumed in the previous step (all waves are past
     // the barrier that ended their reads of it).
-    if (kt + STAGES - 1 < KT) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+    issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int cur = kk & 1;
+      if constexpr (SCHED == 1) __builtin_amdgcn_iglp_opt(0);
+      if constexpr (SCHED == 2) __builtin_amdgcn_iglp_opt(1);
       if (kk < KK - 1) {
         frags(cur ^ 1, st, kk + 1);
       } else {
-        // Step kt+1's tile must have landed (loads issued after it may stay
-        // in flight), then everyone may start reading it.
-        if (kt + STAGES - 1 < KT) stage_barrier<(STAGES - 2) * L>();
-        else stage_barrier<0>();
-        if (kt + 1 < KT) frags(cur ^ 1, (kt + 1) % STAGES, 0);
+        // Step kt+1's tile must have landed (the STAGES-2 younger steps'
+        // loads may stay in flight), then everyone may start reading it.
+        stage_barrier<(STAGES - 2) * L>();
+        frags(cur ^ 1, (kt + 1) % STAGES, 0);
       }
       mma(cur);
+      if constexpr (SCHED == 3) {
+        // 16 MFMAs of this slice: the first 8 each followed by one fragment
+        // read for the next slice; on the first slice the step's
+        // direct-to-LDS loads (2 * 64 / RPI per wave) ride between them too.
+        constexpr int kLoads = 2 * (64 / RPI);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          if (kk == 0 && i < kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+        }
+      }
+      // Nothing crosses a slice boundary: the next slice's MFMAs cannot be
+      // hoisted onto fragments still in flight, so those fragments load
+      // under this slice's MFMAs (a real double buffer).
+      if constexpr (SCHED >= 3) __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // No direct-to-LDS load may still be in flight when the workgroup's LDS
+  // is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue.  acc[a][b][r]: weight row 8*(r/4) + 4*(lane/32) + r%4 of
   // a-block a, x row lane%32 of b-block b.
@@ -255,6 +284,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
 
 constexpr int kBK = 64;
 constexpr int kStages = 2;
+constexpr int kSched = 3;
 
 template <int NB, int ACT, bool BIAS>
 int launch_gemm(GemmArgs g, hipStream_t st) {
@@ -265,8 +295,8 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
   g.tiles_m = (int)tm;
   g.tiles = (int)(tm * tn);
   const int64_t grid = ((g.tiles + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS, kBK, kStages>), dim3((unsigned)grid), dim3(256), 0,
-                     st, g);
+  hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS, kBK, kStages, kSched>), dim3((unsigned)grid),
+                     dim3(256), 0, st, g);
   return launch_status();
 }
 

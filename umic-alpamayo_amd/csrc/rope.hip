@@ -9,10 +9,11 @@
 // head, then the heads of a position, so each load/store instruction of a
 // wavefront covers whole contiguous head rows of q (then k).
 //
-// One block serves P consecutive positions: their cos/sin rows are staged
-// once into LDS (read from HBM once for q AND k, where the reference's
-// per-tensor launches read them twice), then every q and k head of those
-// positions is rotated from registers.  Activations are streamed with
+// One block serves a flat range of 1024 items (4 per thread, all loads in
+// flight together): the cos/sin rows of the positions it touches are staged
+// once into LDS -- read from HBM once for q AND k, where the reference's
+// per-tensor launches read them twice -- and every item is rotated from
+// registers.  Activations are streamed with
 // non-temporal loads/stores: each element is read once and written once.
 //
 // Arithmetic modes (no fp contraction anywhere in this library):
@@ -93,63 +94,61 @@ __device__ __forceinline__ void rotate(const float* xl, const float* xh, const f
 }
 
 template <int MODE, bool CS32, int VEC>
-__global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int P) {
+__global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
   __shared__ float cs_l[kMaxCsFloats];
   __shared__ float sn_l[kMaxCsFloats];
   const int64_t npos = a.B * a.S;
-  const int64_t p0 = (int64_t)blockIdx.x * P;
   const int D = (int)a.D;
   const int half = D / 2;
-
   const int C = half / VEC;  // chunks per half row
   const int ipp = (int)(a.Hq + a.Hk) * C;
   const int nq = (int)a.Hq * C;
-  const int nitems = P * ipp;
-  // Stage cos/sin rows of this block's positions (fp32 in LDS; bf16 widens
+  // This block's flat item range [i0, i1) over (position, head, chunk) and
+  // the positions [p0, p1] it touches.
+  const int64_t nitems = npos * ipp;
+  const int64_t i0 = (int64_t)blockIdx.x * ipb;
+  const int64_t i1 = i0 + ipb < nitems ? i0 + ipb : nitems;
+  const int64_t p0 = i0 / ipp;
+  const int np = (int)((i1 - 1) / ipp - p0 + 1);
+
+  // Stage cos/sin rows of the touched positions (fp32 in LDS; bf16 widens
   // exactly, so TEXT mode still multiplies by the bf16 values).  Run after
   // the first pass's q/k loads are in flight, so both latencies overlap.
   auto stage_tables = [&]() {
-    for (int i = threadIdx.x; i < P * D; i += blockDim.x) {
+    for (int i = threadIdx.x; i < np * D; i += blockDim.x) {
       const int pp = i / D, d = i - pp * D;
       const int64_t p = p0 + pp;
-      float c = 0.f, s = 0.f;
-      if (p < npos) {
-        int64_t b = 0, sidx = p;
-        if (a.B != 1) {
-          b = p / a.S;
-          sidx = p - b * a.S;
-        }
-        const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
-        if constexpr (CS32) {
-          c = static_cast<const float*>(a.cos)[off];
-          s = static_cast<const float*>(a.sin)[off];
-        } else {
-          c = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
-          s = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
-        }
+      int64_t b = 0, sidx = p;
+      if (a.B != 1) {
+        b = p / a.S;
+        sidx = p - b * a.S;
       }
-      cs_l[i] = c;
-      sn_l[i] = s;
+      const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+      if constexpr (CS32) {
+        cs_l[i] = static_cast<const float*>(a.cos)[off];
+        sn_l[i] = static_cast<const float*>(a.sin)[off];
+      } else {
+        cs_l[i] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+        sn_l[i] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+      }
     }
   };
 
   // Each thread takes kItems items per pass; all their loads are issued
-  // before any is consumed (an item past the end re-reads item 0 of the
-  // block, always valid, and stores nothing).
-  for (int base = 0; base < nitems; base += kItems * 256) {
+  // before any is consumed (an item past the range re-reads item i0, always
+  // valid, and stores nothing).
+  for (int64_t base = i0; base < i1; base += kItems * 256) {
     const uint16_t* xs[kItems];
     uint16_t* os[kItems];
     int cofs[kItems], dls[kItems];
     bool ok[kItems];
 #pragma unroll
     for (int u = 0; u < kItems; ++u) {
-      int it = base + u * 256 + (int)threadIdx.x;
-      const int pp0 = it / ipp;
-      ok[u] = it < nitems && p0 + pp0 < npos;
-      if (!ok[u]) it = 0;
-      const int pp = it / ipp;
-      const int j = it - pp * ipp;
-      const int64_t p = p0 + pp;
+      int64_t it = base + u * 256 + (int)threadIdx.x;
+      ok[u] = it < i1;
+      if (!ok[u]) it = i0;
+      const int64_t p = it / ipp;
+      const int j = (int)(it - p * ipp);
       int64_t b = 0, sidx = p;
       if (a.B != 1) {
         b = p / a.S;
@@ -166,7 +165,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int P) {
         os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
       }
       dls[u] = c * VEC;
-      cofs[u] = pp * D;
+      cofs[u] = (int)(p - p0) * D;
     }
     float xl[kItems][VEC], xh[kItems][VEC];
 #pragma unroll
@@ -174,7 +173,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int P) {
       Chunk<VEC>::load(xs[u] + dls[u], xl[u]);
       Chunk<VEC>::load(xs[u] + half + dls[u], xh[u]);
     }
-    if (base == 0) {  // uniform: every thread takes the first pass
+    if (base == i0) {  // uniform: every thread takes the first pass
       stage_tables();
       __syncthreads();
     }
@@ -196,15 +195,16 @@ template <int MODE, bool CS32, int VEC>
 int launch_rope(const RopeArgs& a, hipStream_t st) {
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
-  // As many whole positions as fit kItems items per thread (one pass for
-  // the usual head counts), bounded by the LDS tables.
-  int64_t P = (kItems * 256) / ipp;
-  if (P < 1) P = 1;
-  if (P * a.D > kMaxCsFloats) P = kMaxCsFloats / a.D;
-  const int64_t blocks = (npos + P - 1) / P;
+  // kItems items per thread in one pass; the positions a range touches
+  // (at most ipb / ipp + 2) must fit the LDS tables.
+  int64_t ipb = kItems * 256;
+  const int64_t max_pos = kMaxCsFloats / a.D;
+  if (ipb / ipp + 2 > max_pos) ipb = (max_pos - 2) * ipp;
+  if (ipb < 1) return UMIC_ERR_UNSUPPORTED;
+  const int64_t blocks = (npos * ipp + ipb - 1) / ipb;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((rope_qk_kernel<MODE, CS32, VEC>), dim3((unsigned)blocks), dim3(256), 0, st,
-                     a, (int)P);
+                     a, (int)ipb);
   return launch_status();
 }
 
@@ -230,7 +230,7 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   if (mode != UMIC_ROPE_TEXT && mode != UMIC_ROPE_VISION) return UMIC_ERR_INVALID_ARG;
   if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
   if (mode == UMIC_ROPE_TEXT && cs_fp32) return UMIC_ERR_UNSUPPORTED;
-  if (D % 2 != 0 || D > kMaxCsFloats) return UMIC_ERR_UNSUPPORTED;
+  if (D % 2 != 0 || D > kMaxCsFloats / 4) return UMIC_ERR_UNSUPPORTED;
   if ((Hq + Hk) * (D / 2) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
   if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;  // empty: pointers may be null
   if (!cos || !sin) return UMIC_ERR_INVALID_ARG;

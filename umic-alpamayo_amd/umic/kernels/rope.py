@@ -25,6 +25,8 @@ import torch
 from umic import _lib
 from umic.kernels._common import require_device
 
+MAX_HEAD_DIM = 1024  # cos/sin rows of a block's positions are staged in LDS
+
 
 def _strides_bsh(t: torch.Tensor, order: str) -> tuple[int, int, int]:
     """(batch, position, head) element strides of t laid out as `order`."""
@@ -71,6 +73,7 @@ def text_rope_eligible(q, k, cos, sin, unsqueeze_dim=1) -> bool:
         return False
     B, _, S, D = q.shape
     return (k.shape[0] == B and k.shape[2] == S and k.shape[3] == D and D % 2 == 0
+            and D <= MAX_HEAD_DIM
             and cos.shape[1] == S and cos.shape[2] == D and cos.shape[0] in (1, B)
             and q.stride(-1) == 1 and k.stride(-1) == 1 and _same_table_layout(cos, sin)
             and k.device == q.device and cos.device == q.device)
@@ -85,7 +88,8 @@ def vision_rope_eligible(q, k, cos, sin) -> bool:
             and cos.dtype in (torch.float32, torch.bfloat16)):
         return False
     S, _, D = q.shape
-    return (k.shape[0] == S and k.shape[2] == D and D % 2 == 0 and tuple(cos.shape) == (S, D)
+    return (k.shape[0] == S and k.shape[2] == D and D % 2 == 0 and D <= MAX_HEAD_DIM
+            and tuple(cos.shape) == (S, D)
             and q.stride(-1) == 1 and k.stride(-1) == 1 and _same_table_layout(cos, sin)
             and k.device == q.device and cos.device == q.device)
 
