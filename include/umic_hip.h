@@ -124,7 +124,7 @@ int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void* k_out,
  * out = act(x @ w^T + bias), bf16 in/out, fp32 accumulation on MFMA.
  * x: [M, K] row stride ldx; w: [N, K] (nn.Linear layout) row stride ldw;
  * bias: [N] bf16 or NULL; out: [M, N] row stride ldo.
- * Requires K % 64 == 0, N % 8 == 0, ldx/ldw/ldo % 8 == 0 and 16-byte
+ * Requires K % 32 == 0, N % 8 == 0, ldx/ldw/ldo % 8 == 0 and 16-byte
  * aligned pointers (else UMIC_ERR_UNSUPPORTED).
  * Replaces: kernels/linear.py:118-145 (linear_triton), kernel
  * kernels/linear.py:32-90; caller integrate.py:98-107.

@@ -90,8 +90,8 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_add_rmsnorm_bf16(fake, None, fake, fake, fake, 4, 64, 64, 64, 64, 64,
                                      1e-6, None) == E_ARG
     assert lib.umic_layernorm_bf16(fake, fake, None, fake, 4, 64, 64, 64, 1e-6, None) == E_ARG
-    # linear: K not a multiple of 64, N not a multiple of 8, bad act
-    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 96, 96, 96, 64, 0, None) == E_UNS
+    # linear: K not a multiple of 32, N not a multiple of 8, bad act
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 80, 80, 80, 64, 0, None) == E_UNS
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 60, 128, 128, 128, 60, 0, None) == E_UNS
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 7, None) == E_ARG
     assert lib.umic_linear_bf16(fake, fake, None, fake, 0, 64, 128, 128, 128, 64, 0, None) == 0

@@ -32,7 +32,7 @@ def _check_vs_oracle(out, ref_bits):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 520, 320), (256, 256, 64), (64, 8, 128), (1, 64, 256),
-                                   (513, 1024, 512), (0, 64, 64)])
+                                   (513, 1024, 512), (0, 64, 64), (130, 72, 32), (300, 264, 96)])
 def test_linear_vs_oracle(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.05, gen=g)
@@ -65,7 +65,8 @@ def test_linear_strided_x_and_leading_dims():
                                                        0, fused=True))
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 520, 320), (64, 128, 64), (257, 384, 1024), (1, 8, 64)])
+@pytest.mark.parametrize("M,N,K", [(300, 520, 320), (64, 128, 64), (257, 384, 1024), (1, 8, 64),
+                                   (65, 200, 160)])
 def test_gate_silu_mul_vs_oracle(M, N, K):
     g = torch.Generator().manual_seed(M * 3 + N + K)
     x = bf16_randn(M, K, gen=g)

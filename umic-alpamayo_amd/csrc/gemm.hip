@@ -14,14 +14,10 @@
 // is written.  Each wavefront computes 128 weight rows x 128 x rows with a
 // 4 x 4 grid of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).
 //
-// Data movement.  K advances in steps of 64: every thread fetches eight
-// 16-byte chunks of the weight tile and eight of the x tile per step
-// (global_load_dwordx4), parks them in registers while the MFMAs of the
-// previous step run, then writes them to the other half of a double-buffered
-// LDS (2 x 64 KB) -- one barrier per K step.  LDS rows are 128 bytes with the
-// 16-byte chunk index XOR-swizzled by (row & 7), so both the row-wise writes
-// and the 32-row fragment reads hit 8 distinct chunk slots per 8 lanes
-// (bank-conflict free).  The MFMA A operand is the weight tile, B the x tile,
+// Data movement.  Tiles move global -> LDS with direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds, no register staging) through a multi-stage
+// LDS ring, one barrier per K step; LDS rows are XOR-swizzled so fragment
+// reads are bank-conflict free (see Geo).  The MFMA A operand is the weight tile, B the x tile,
 // so each lane's 16 outputs are 4 runs of 4 consecutive output columns:
 // the epilogue writes 8-byte packed bf16 runs.
 //
@@ -54,17 +50,19 @@ struct GemmArgs {
 
 // LDS geometry for a K step of BK elements.  A tile row is BK bf16 = BK*2
 // bytes = CPR 16-byte chunks; one direct-to-LDS wave instruction moves
-// 64 x 16 B = 1 KB = RPI consecutive rows.  Chunks are XOR-swizzled within a
-// row so that the 8 lanes serviced together by a 128-byte LDS access (the
-// MFMA fragment reads walk 8 consecutive rows at a fixed chunk) land on 8
-// distinct 16-byte bank groups.
+// 64 x 16 B = 1 KB = RPI consecutive rows.  gfx950's LDS serves 16 lanes x
+// 16 B = 256 B (64 banks) per cycle, and an MFMA fragment read has those 16
+// lanes on 16 consecutive rows at one chunk, so the chunk is XOR-swizzled
+// to give every row of a 256-byte bank line group a distinct 16-byte slot:
+// 128 B rows pair up per bank line, so rows r and r+2, r+4, ... r+14 must
+// differ -> (row >> 1) & 7; 64 B rows come four to a bank line -> (row >> 2) & 3.
 template <int BK>
 struct Geo {
   static constexpr int CPR = BK / 8;
   static constexpr int RPI = 64 / CPR;
   static __device__ __forceinline__ int swz(int row) {
-    if constexpr (BK == 64) return row & 7;          // 128 B rows
-    else return (row >> 1) & 3;                      // 64 B rows, 2 per 128 B
+    if constexpr (BK == 64) return (row >> 1) & 7;
+    else return (row >> 2) & 3;
   }
   static __device__ __forceinline__ int slot(int row, int chunk) {
     return row * CPR + (chunk ^ swz(row));
@@ -87,7 +85,8 @@ __device__ __forceinline__ void stage_barrier() {
 // direct-to-LDS loads inside a K step: 0 leaves it to the compiler, 1 and 2
 // are the compiler's built-in GEMM strategies (iglp_opt 0 / 1), 3 pins one
 // LDS read (and on the first slice one load) after each of the first MFMAs
-// and fences each K slice, 4 only fences each K slice.
+// and fences each K slice, 4 only fences each K slice, 5 is 3 with the K
+// step's loads issued an equal share per slice, spread between the MFMAs.
 template <int NB, int ACT, bool BIAS, int BK, int STAGES, int SCHED>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   using G = Geo<BK>;
@@ -132,26 +131,30 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
 
   // This wave DMAs tile rows [wave*64, wave*64+64) of both operands.  Lane
   // l writes LDS slot l % CPR of row l / CPR of each 1 KB group, so it
-  // fetches the chunk that the swizzle places there.
+  // fetches the chunk that the swizzle places there (the swizzle of row
+  // wave*64 + j*RPI + lr depends only on j and lr).
   const int lr = lane / CPR;
-  const int lchunk = (lane % CPR) ^ G::swz(lr);
   const int wrow0 = NB == 1 ? n0 + wave * 64 : n0 + (wave & 1) * 64;
   const int xrow0 = m0 + wave * 64;
-  const int woff = (int)(((int64_t)(wrow0 + lr) * ldw + lchunk * 8) * 2);
-  const int xoff = (int)(((int64_t)(xrow0 + lr) * g.ldx + lchunk * 8) * 2);
+  const int woff = (int)((int64_t)(wrow0 + lr) * ldw * 2);
+  const int xoff = (int)((int64_t)(xrow0 + lr) * g.ldx * 2);
   const int wstep = (int)(RPI * ldw * 2), xstep = (int)(RPI * g.ldx * 2);
+  auto chunk_off = [&](int j) { return ((lane % CPR) ^ G::swz(j * RPI + lr)) * 16; };
 
-  auto issue = [&](int stage, int k0) {
+  // Issue rows-blocks [j0, j1) of this wave's share of a K step's tiles.
+  auto issue_part = [&](int stage, int k0, int j0, int j1) {
     lds_void* dw = (lds_void*)&lds[stage][0][wave * 64 * CPR];
     lds_void* dx = (lds_void*)&lds[stage][1][wave * 64 * CPR];
 #pragma unroll
-    for (int j = 0; j < 64 / RPI; ++j) {
+    for (int j = j0; j < j1; ++j) {
+      const int co = chunk_off(j) + k0 * 2;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)((__attribute__((address_space(3))) char*)dw + j * 1024),
-                                               16, woff + j * wstep + k0 * 2, 0, 0, 0);
+                                               16, woff + j * wstep + co, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)((__attribute__((address_space(3))) char*)dx + j * 1024),
-                                               16, xoff + j * xstep + k0 * 2, 0, 0, 0);
+                                               16, xoff + j * xstep + co, 0, 0, 0);
     }
   };
+  auto issue = [&](int stage, int k0) { issue_part(stage, k0, 0, 64 / RPI); };
 
   // Fragment rows: a-blocks (weights) and b-blocks (x), 32 rows each.
   int arow[4], brow[4];
@@ -204,11 +207,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   for (int kt = 0; kt < KT; ++kt) {
     const int st = kt % STAGES;
     // Refill the buffer consumed in the previous step (all waves are past
-    // the barrier that ended their reads of it).
-    issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+    // the barrier that ended their reads of it): all at once, or (SCHED 5)
+    // an equal share in each K slice so the loads issue evenly between MFMAs.
+    constexpr int kJ = 64 / RPI;  // row blocks per operand per wave
+    if constexpr (SCHED != 5) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int cur = kk & 1;
+      if constexpr (SCHED == 5)
+        issue_part((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK, kk * kJ / KK,
+                   (kk + 1) * kJ / KK);
       if constexpr (SCHED == 1) __builtin_amdgcn_iglp_opt(0);
       if constexpr (SCHED == 2) __builtin_amdgcn_iglp_opt(1);
       if (kk < KK - 1) {
@@ -230,6 +238,17 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
           if (kk == 0 && i < kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+        }
+      }
+      if constexpr (SCHED == 5) {
+        // 16 MFMAs of this slice, one fragment read after each of the first
+        // 8 and this slice's share of the loads spread evenly between them.
+        constexpr int kLoadsPerSlice = 2 * kJ / KK;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          if (i % (16 / kLoadsPerSlice) == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
       }
       // Nothing crosses a slice boundary: the next slice's MFMAs cannot be
@@ -282,9 +301,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   }
 }
 
-constexpr int kBK = 64;
-constexpr int kStages = 2;
-constexpr int kSched = 3;
+constexpr int kBK = 32;
+constexpr int kStages = 4;
+constexpr int kSched = 5;
 
 template <int NB, int ACT, bool BIAS>
 int launch_gemm(GemmArgs g, hipStream_t st) {
@@ -300,8 +319,9 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
   return launch_status();
 }
 
-// Buffer-resource offsets are 32-bit: every operand (rows x leading dim)
-// must stay below 2 GiB, and tile row offsets below 2^31 as well.
+// Buffer-resource offsets are 32-bit: every operand (rows x leading dim),
+// plus the K overrun of the last steps' refills (STAGES-1 steps past K),
+// must stay below 2 GiB.
 bool gemm_shape_ok(const void* x, const void* w0, const void* w1, const void* out, int64_t M,
                    int64_t N, int64_t K, int64_t ldx, int64_t ldw0, int64_t ldw1, int64_t ldo) {
   if (K % kBK != 0 || N % 8 != 0) return false;
@@ -309,7 +329,9 @@ bool gemm_shape_ok(const void* x, const void* w0, const void* w1, const void* ou
   if (!aligned16(x) || !aligned16(w0) || !aligned16(w1) || !aligned16(out)) return false;
   const int64_t lim = (int64_t)1 << 30;  // elements (2 GiB of bf16)
   const int64_t mpad = (M + kBM - 1) / kBM * kBM, npad = (N + kBW - 1) / kBW * kBW;
-  if (mpad * ldx >= lim || npad * ldw0 >= lim || npad * ldw1 >= lim) return false;
+  const int64_t slack = (int64_t)kStages * kBK;
+  if (mpad * ldx + slack >= lim || npad * ldw0 + slack >= lim || npad * ldw1 + slack >= lim)
+    return false;
   return true;
 }
 

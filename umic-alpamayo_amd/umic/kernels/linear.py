@@ -15,7 +15,7 @@ import torch
 from umic import _lib
 from umic.kernels._common import ld, require_device, rows2d
 
-K_MULTIPLE = 64  # the kernel's K step
+K_MULTIPLE = 32  # the kernel's K step
 N_MULTIPLE = 8   # 16-byte output runs
 
 
