@@ -71,15 +71,15 @@ struct GemmArgs {
 
 // LDS geometry of one operand tile of a K step: a row is BK bf16 = 64 bytes
 // = CPR 16-byte chunks; one direct-to-LDS wave instruction moves 64 x 16 B
-// = 1 KB = RPI consecutive rows.  gfx950's LDS serves 16 lanes x 16 B =
-// 256 B (64 banks) per cycle, and a fragment read has those 16 lanes on 16
-// consecutive rows at one chunk; four 64-byte rows share a 256-byte bank
-// line, so the chunk is XOR-swizzled by (row >> 2) & 3 and the 16 rows land
-// on 16 distinct 16-byte bank groups.
+// = 1 KB = RPI consecutive rows.  A fragment read (ds_read_b128) has lane l
+// on row l % 16, chunk l / 16.  The chunk is XOR-swizzled by (row >> 1) & 3:
+// measured with SQ_LDS_BANK_CONFLICT on gfx950, that read pattern is
+// conflict-free under this swizzle, 2-way under (row >> 2) & 3, row & 3 or
+// none.  Direct-to-LDS writes are 1 KB contiguous and conflict-free.
 struct Geo {
   static constexpr int CPR = kBK / 8;
   static constexpr int RPI = 64 / CPR;
-  static __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+  static __device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
   static __device__ __forceinline__ int slot(int row, int chunk) {
     return row * CPR + (chunk ^ swz(row));
   }
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(nrows * ld * 2), 0x00020000);
   // Lane l writes LDS slot l % CPR of row l / CPR of each 1 KB group, so it
   // fetches the chunk the swizzle places there (the swizzle of tile row
-  // q*64 + j*RPI + lr depends only on j and lr).
+  // q*64 + j*RPI + lr depends only on lr).
   const int lr = lane / CPR;
   const int off0 = (int)((int64_t)(row0 + lr) * ld * 2);
   const int rstep = (int)(RPI * ld * 2);
