@@ -135,6 +135,33 @@ int umic_linear_bf16(const void* x, const void* w, const void* bias, void* out,
                      int act, void* stream);
 
 /*
+ * Bytes of device workspace umic_linear_ws_bf16 uses for this shape on the
+ * current device: nonzero when the output has fewer 256 x 256 tiles than
+ * the device has CUs (then a stream-K schedule spreads the K loop over every
+ * CU), 0 when the data-parallel kernel is used and no workspace is needed.
+ * Host-only query; enqueues nothing.
+ */
+int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * umic_linear_bf16 with a caller-provided workspace for the stream-K
+ * schedule.  Same arguments, numerics and shape rules; results are
+ * deterministic (split tiles sum their K segments in a fixed order).
+ * workspace: >= umic_linear_workspace_bytes(M, N, K) bytes, 256-byte
+ * aligned, ALL ZERO before its first use; every call leaves its counters at
+ * zero again, so one workspace serves any number of calls that do not
+ * overlap in time (e.g. all calls on one stream).  Calls that may run
+ * concurrently need separate workspaces.  A smaller (or NULL) workspace, or
+ * a shape the data-parallel kernel serves better, runs umic_linear_bf16.
+ * Replaces: kernels/linear.py:118-145 (linear_triton), as umic_linear_bf16;
+ * caller integrate.py:98-107.
+ */
+int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* out,
+                        int64_t M, int64_t N, int64_t K,
+                        int64_t ldx, int64_t ldw, int64_t ldo,
+                        int act, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Fused P5 MLP front half: out = silu(x @ wg^T) * (x @ wu^T), one bf16
  * rounding of the fp32 product.  wg, wu: [N, K] nn.Linear weights (the
  * reference passes them as .t() views; same memory).

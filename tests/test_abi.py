@@ -36,7 +36,8 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
               "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
-              "umic_gate_silu_mul_bf16", "umic_version", "umic_error_string"):
+              "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
+              "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -97,6 +98,17 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_linear_bf16(fake, fake, None, fake, 0, 64, 128, 128, 128, 64, 0, None) == 0
     assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
                                        None) == E_ARG
+    # stream-K linear: same validation; a negative workspace size is rejected
+    assert lib.umic_linear_workspace_bytes(0, 64, 128) == 0
+    assert lib.umic_linear_workspace_bytes(64, 64, 100) == 0  # K not a multiple of 32
+    assert lib.umic_linear_ws_bf16(fake, fake, None, fake, 8, 64, 80, 80, 80, 64, 0, None, 0,
+                                   None) == E_UNS
+    assert lib.umic_linear_ws_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 7, None, 0,
+                                   None) == E_ARG
+    assert lib.umic_linear_ws_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 0, fake, -1,
+                                   None) == E_ARG
+    assert lib.umic_linear_ws_bf16(None, None, None, None, 0, 64, 128, 128, 128, 64, 0, None, 0,
+                                   None) == 0
     # rope: odd head dim, text mode with fp32 tables, bad mode
     args = [fake, fake, fake, fake, fake, fake]
     strides = [0] * 12 + [0, 0]

@@ -88,6 +88,75 @@ def test_gate_silu_mul_row_major_kn_weights():
     _check_vs_oracle(y, oracle.gate_silu_mul(bits(x), bits(wg_kn.t()), bits(wu_kn.t())))
 
 
+# Shapes with fewer 256 x 256 tiles than CUs and a long K loop take the
+# stream-K schedule (umic_linear_workspace_bytes > 0); on a 256-CU MI355X
+# these split tiles into 2 or 3 K segments, so every reduction order (the
+# last-arriving segment first, middle or last) is exercised.
+SK_SHAPES = [(300, 264, 12288, 2), (700, 256, 12288, 1), (200, 392, 12288, 1)]
+
+
+def _sk_bytes(M, N, K):
+    from umic import _lib
+
+    return _lib.lib().umic_linear_workspace_bytes(M, N, K)
+
+
+@pytest.mark.parametrize("M,N,K,calls", SK_SHAPES)
+def test_linear_stream_k_vs_oracle(M, N, K, calls):
+    assert _sk_bytes(M, N, K) > 0, "shape no longer takes the stream-K schedule"
+    for seed in range(calls):  # back-to-back calls reuse the stream's workspace
+        g = torch.Generator().manual_seed(M + N + K + seed)
+        x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.02, gen=g)
+        y = linear.linear_hip(x.to(DEV), w.to(DEV))
+        torch.cuda.synchronize()
+        _check_vs_oracle(y, oracle.linear(bits(x), bits(w), None, 0, fused=True))
+
+
+def test_linear_stream_k_bias_gelu_vs_oracle():
+    M, N, K = 300, 264, 12288
+    assert _sk_bytes(M, N, K) > 0
+    g = torch.Generator().manual_seed(11)
+    x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.02, gen=g)
+    b = bf16_randn(N, scale=0.5, gen=g)
+    y = linear.linear_hip(x.to(DEV), w.to(DEV), b.to(DEV), act="gelu")
+    torch.cuda.synchronize()
+    _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), 1, fused=True))
+
+
+def test_stream_k_deterministic_and_close_to_data_parallel():
+    """down_proj shape: stream-K is bit-reproducible, and
+    within fp32 summation-order noise of the data-parallel kernel."""
+    from umic import _lib
+
+    M, N, K = 3100, 4096, 12288
+    assert _sk_bytes(M, N, K) > 0
+    torch.manual_seed(5)
+    x = torch.randn(M, K).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K) * 0.02).to(torch.bfloat16).to(DEV)
+    y1 = linear.linear_hip(x, w)
+    y2 = linear.linear_hip(x, w)
+    ydp = torch.empty_like(y1)
+    _lib.call("umic_linear_bf16", x.data_ptr(), w.data_ptr(), None, ydp.data_ptr(), M, N, K,
+              K, K, N, 0, _lib.stream_of(x))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    d = ulp(bits(y1), bits(ydp))
+    assert (d <= 1).mean() > 0.999, np.bincount(d.ravel())[:8]
+    # larger ulp counts only where the output is near zero (cancellation):
+    # no difference exceeds one bf16 ulp of the largest output (2^-7 relative)
+    assert ((y1.float() - ydp.float()).abs().max() / ydp.float().abs().max()).item() <= 2.0 ** -7
+
+
+def test_down_proj_full_shape_vs_fp32():
+    """BASELINE config 3 down_proj (the stream-K linear) against fp32 torch."""
+    torch.manual_seed(6)
+    x = torch.randn(3100, 12288).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(4096, 12288) * 0.02).to(torch.bfloat16).to(DEV)
+    y = linear.linear_hip(x, w)
+    ref = x.float() @ w.float().t()
+    assert max_rel_err(y, ref) <= TOL and rel_err(y, ref) <= TOL
+
+
 def _fp32_ref_linear(x, w):
     return (x.float() @ w.float().t())
 

@@ -36,6 +36,7 @@ def _inputs(seed):
         "v": bf16_randn(64, 1280, gen=g),
         "vr": bf16_randn(64, 1280, gen=g),
         "x": bf16_randn(128, 512, gen=g),
+        "xs": bf16_randn(300, 12288, gen=g),
     }
 
 
@@ -51,6 +52,7 @@ def _step(t, p):
     out["ln"] = layernorm.layernorm_hip(t["v"], p["lw"], p["lb"], 1e-6)
     out["aln"], out["as"] = layernorm.add_layernorm_hip(t["v"], t["vr"], p["lw"], p["lb"], 1e-6)
     out["lin"] = linear.linear_hip(t["x"], p["wl"])
+    out["lin_sk"] = linear.linear_hip(t["xs"], p["wsk"])  # stream-K schedule
     out["p5"] = fused_ffn.gate_silu_mul_hip(t["x"], p["wg"].t(), p["wu"].t())
     return out
 
@@ -65,7 +67,11 @@ def test_fused_kernels_replay_in_hip_graph():
         "wl": bf16_randn(256, 512, scale=0.05, gen=g).to(DEV),
         "wg": bf16_randn(384, 512, scale=0.05, gen=g).to(DEV),
         "wu": bf16_randn(384, 512, scale=0.05, gen=g).to(DEV),
+        "wsk": bf16_randn(264, 12288, scale=0.02, gen=g).to(DEV),
     }
+    from umic import _lib
+
+    assert _lib.lib().umic_linear_workspace_bytes(300, 264, 12288) > 0
     static = {k: v.to(DEV) for k, v in _inputs(0).items()}
     # warm up on a side stream (as torch.cuda.graphs recommends), then capture
     side = torch.cuda.Stream()

@@ -43,6 +43,8 @@
 // tiles one XCD runs together share x and weight slabs in its 4 MB L2.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace umic {
 namespace {
 
@@ -96,189 +98,401 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
 }
 
-// Hazards of the ring.  Step j's stage is read in phases 2j-1 (group 0) and
-// 2j (group 1) and refilled (as step j + S) in phases 2j+2 / 2j+3, after
-// two barriers, each preceded by lgkmcnt(0).  Step j+1's two load batches
-// were issued in phases 2(j+1-D) (weights, group 1) and 2(j+1-D)+1 (x,
-// group 0).  At the barrier ending phase 2j, group 1 has D batches
-// outstanding at most and waits for all but D-1; group 0 has issued one
-// batch fewer and waits for all but D-2: both halves of step j+1 have
-// landed before anyone reads it in phase 2j+1.  Barriers ending odd phases
-// need no load wait (the same counts are already met there).
-template <int NB, int ACT, bool BIAS>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
-  using G = Geo;
-  constexpr int CPR = G::CPR, RPI = G::RPI;
-  constexpr int D = kAhead, S = kStages;
-  constexpr int LB = 64 / RPI;  // direct-to-LDS loads per wave per batch
-  // [stage][operand: 0 weights, 1 x][row * CPR + slot], 16-byte units
-  __shared__ u32x4 lds[S][2][kBM * CPR];
+typedef u32x4 LdsRing[kStages][2][kBM * Geo::CPR];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  // wave-uniform (scalar) wave index: the operand pointer chosen from it
-  // must live in SGPRs for the buffer resource
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, q = wave & 3;
-  const int wm = q & 1, wn = q >> 1;
-
-  // XCD-aware remap: physical ids b, b+8, b+16, ... (one XCD) take
-  // consecutive logical tiles; logical tiles run in groups of kGroupM tile
-  // rows, m fastest inside a group, so the ~32 tiles an XCD holds at once
-  // form a kGroupM x 8 block whose x and weight slabs its L2 shares.
-  const int per_xcd = (g.tiles + 7) >> 3;
-  const int logical = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
-  if (logical >= g.tiles) return;
+// Tile origin of logical tile t in the grouped order: groups of kGroupM tile
+// rows, m fastest inside a group.
+__device__ __forceinline__ void tile_origin(const GemmArgs& g, int t, int bw, int& m0, int& n0) {
   const int tiles_n = g.tiles / g.tiles_m;
-  const int group = logical / (kGroupM * tiles_n);
+  const int group = t / (kGroupM * tiles_n);
   const int first_m = group * kGroupM;
   const int gm = min(g.tiles_m - first_m, kGroupM);
-  const int in_group = logical - group * kGroupM * tiles_n;
-  const int tm = first_m + in_group % gm;
-  const int tn = in_group / gm;
-  const int m0 = tm * kBM;
-  const int n0 = tn * (NB == 1 ? kBW : kBW / 2);
+  const int in_group = t - group * kGroupM * tiles_n;
+  m0 = (first_m + in_group % gm) * kBM;
+  n0 = (in_group / gm) * bw;
+}
 
-  // The operand this wave streams: group 1 the weight tile (for P5 waves
-  // 0-1 of the group the gate rows, 2-3 the up rows), group 0 the x tile,
-  // 64 rows per wave.  Rows past M / N read as zero.
-  const int opnd = grp ? 0 : 1;
-  const bool up = NB == 2 && grp && q >= 2;
-  const uint16_t* src = grp ? (up ? g.w1 : g.w0) : g.x;
-  const int64_t ld = grp ? (up ? g.ldw1 : g.ldw0) : g.ldx;
-  const int64_t nrows = grp ? g.N : g.M;
-  const int row0 = grp ? (NB == 1 ? n0 + q * 64 : n0 + (q & 1) * 64) : m0 + q * 64;
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(nrows * ld * 2), 0x00020000);
-  // Lane l writes LDS slot l % CPR of row l / CPR of each 1 KB group, so it
-  // fetches the chunk the swizzle places there (the swizzle of tile row
-  // q*64 + j*RPI + lr depends only on lr).
-  const int lr = lane / CPR;
-  const int off0 = (int)((int64_t)(row0 + lr) * ld * 2);
-  const int rstep = (int)(RPI * ld * 2);
-  auto issue = [&](int stage, int k0) {
+// XCD-aware remap of a physical workgroup id: ids b, b+8, b+16, ... (one
+// XCD, which the hardware fills round-robin) take consecutive logical ids,
+// so what one XCD runs together is a contiguous run of the grouped order
+// (for tiles: a kGroupM x 8 block whose x and weight slabs its L2 shares).
+__device__ __forceinline__ int xcd_remap(int count) {
+  const int per_xcd = (count + 7) >> 3;
+  return (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+}
+
+// One wavefront's share of the ping-pong pipeline for one tile: which
+// operand rows it streams into LDS, which fragments it reads, and its
+// 8 x 4 blocks of 16x16 accumulators.
+//
+// Hazards of the ring (per K segment run by run()).  Step j's stage is read
+// in phases 2j-1 (group 0) and 2j (group 1) and refilled (as step j + S) in
+// phases 2j+2 / 2j+3, after two barriers, each preceded by lgkmcnt(0).
+// Step j+1's two load batches were issued in phases 2(j+1-D) (weights,
+// group 1) and 2(j+1-D)+1 (x, group 0).  At the barrier ending phase 2j,
+// group 1 has D batches outstanding at most and waits for all but D-1;
+// group 0 has issued one batch fewer and waits for all but D-2: both halves
+// of step j+1 have landed before anyone reads it in phase 2j+1.  Barriers
+// ending odd phases need no load wait (the same counts are already met).
+template <int NB>
+struct Pipe {
+  static constexpr int CPR = Geo::CPR, RPI = Geo::RPI;
+  static constexpr int D = kAhead, S = kStages;
+  static constexpr int LB = 64 / RPI;  // direct-to-LDS loads per wave per batch
+
+  int lane, grp, q, wm, wn, frow, fch, lr, opnd;
+  int arow[8], brow[4];
+  // The streamed operand; its buffer resource is built inside run() (a
+  // resource held in this struct loses its wave-uniformity and every load
+  // turns into a waterfall loop).
+  const uint16_t* src;
+  int nbytes, off0, rstep;
+  f32x4_t acc[8][4];
+  bf16x8_t fa[8], fb[4];
+
+  __device__ __forceinline__ void init(int tid) {
+    lane = tid & 63;
+    // wave-uniform (scalar) wave index: the operand pointer chosen from it
+    // must live in SGPRs for the buffer resource
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    grp = wave >> 2;
+    q = wave & 3;
+    wm = q & 1;
+    wn = q >> 1;
+    opnd = grp ? 0 : 1;
+    lr = lane / CPR;
+    frow = lane & 15;  // fragment row of this lane
+    fch = lane >> 4;   // its 8-element K chunk
+    // Fragment blocks of 16 rows: weights (A) -- linear: rows wn*128 +
+    // a*16; P5: gate rows wn*64 + a*16 (a < 4) and the matching up rows
+    // 128 + wn*64 + (a-4)*16 -- and x (B): rows wm*128 + grp*64 + b*16.
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+      arow[a] = NB == 1 ? wn * 128 + a * 16 : (a >> 2) * 128 + wn * 64 + (a & 3) * 16;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) brow[b] = wm * 128 + grp * 64 + b * 16;
+  }
+
+  // The operand this wave streams for the tile at (m0, n0): group 1 the
+  // weight tile (for P5 waves 0-1 of the group the gate rows, 2-3 the up
+  // rows), group 0 the x tile, 64 rows per wave.  Rows past M / N read as
+  // zero.  Lane l writes LDS slot l % CPR of row l / CPR of each 1 KB
+  // group, so it fetches the chunk the swizzle places there (the swizzle of
+  // tile row q*64 + j*RPI + lr depends only on lr).
+  __device__ __forceinline__ void bind(const GemmArgs& g, int m0, int n0) {
+    const bool up = NB == 2 && grp && q >= 2;
+    src = grp ? (up ? g.w1 : g.w0) : g.x;
+    const int64_t ld = grp ? (up ? g.ldw1 : g.ldw0) : g.ldx;
+    const int64_t nrows = grp ? g.N : g.M;
+    const int row0 = grp ? (NB == 1 ? n0 + q * 64 : n0 + (q & 1) * 64) : m0 + q * 64;
+    nbytes = (int)(nrows * ld * 2);
+    off0 = (int)((int64_t)(row0 + lr) * ld * 2);
+    rstep = (int)(RPI * ld * 2);
+  }
+
+  __device__ __forceinline__ void issue(LdsRing& lds, __amdgpu_buffer_rsrc_t rs, int stage,
+                                        int k0) {
     lds_char* d = (lds_char*)&lds[stage][opnd][q * 64 * CPR];
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
-      const int co = ((lane % CPR) ^ G::swz(j * RPI + lr)) * 16 + k0 * 2;
+      const int co = ((lane % CPR) ^ Geo::swz(j * RPI + lr)) * 16 + k0 * 2;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(d + j * 1024), 16,
                                                off0 + j * rstep + co, 0, 0, 0);
     }
-  };
+  }
 
-  // Fragment blocks of 16 rows: weights (A) -- linear: rows wn*128 + a*16;
-  // P5: gate rows wn*64 + a*16 (a < 4) and the matching up rows
-  // 128 + wn*64 + (a-4)*16 -- and x (B): rows wm*128 + grp*64 + b*16.
-  int arow[8], brow[4];
-#pragma unroll
-  for (int a = 0; a < 8; ++a)
-    arow[a] = NB == 1 ? wn * 128 + a * 16 : (a >> 2) * 128 + wn * 64 + (a & 3) * 16;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) brow[b] = wm * 128 + grp * 64 + b * 16;
-  const int frow = lane & 15;  // fragment row of this lane
-  const int fch = lane >> 4;   // its 8-element K chunk
-
-  f32x4_t acc[8][4];
-#pragma unroll
-  for (int a = 0; a < 8; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[a][b][r] = 0.f;
-
-  bf16x8_t fa[8], fb[4];
-  auto frags = [&](int stage) {
+  __device__ __forceinline__ void frags(LdsRing& lds, int stage) {
 #pragma unroll
     for (int a = 0; a < 8; ++a)
-      fa[a] = __builtin_bit_cast(bf16x8_t, lds[stage][0][G::slot(arow[a] + frow, fch)]);
+      fa[a] = __builtin_bit_cast(bf16x8_t, lds[stage][0][Geo::slot(arow[a] + frow, fch)]);
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      fb[b] = __builtin_bit_cast(bf16x8_t, lds[stage][1][G::slot(brow[b] + frow, fch)]);
-  };
-  auto compute = [&]() {
+      fb[b] = __builtin_bit_cast(bf16x8_t, lds[stage][1][Geo::slot(brow[b] + frow, fch)]);
+  }
+
+  __device__ __forceinline__ void compute() {
 #pragma unroll
     for (int a = 0; a < 8; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-  };
-
-  const int KT = (int)(g.K / kBK);
-  // Prologue: D steps in flight, step 0 landed, group 0 holds its step-0
-  // fragments.  The loop stays branch-free: the last D steps still refill
-  // stages that are never read again, from offsets past K (in-range data or
-  // range-checked zeros), and group 0 reads step-KT fragments it never uses.
-#pragma unroll
-  for (int s = 0; s < D; ++s) issue(s, s * kBK);
-  stage_barrier<(D - 1) * LB>();
-  if (grp == 0) frags(0);
-  stage_barrier<(D - 1) * LB>();
-
-  // One straight loop per group (the hardware barrier counts arrivals, not
-  // program points; both loops pass the same barriers), so the fragments
-  // stay loop-carried in place.  sched_barrier keeps every MFMA in its phase.
-  if (grp == 0) {
-    for (int j = 0; j < KT; ++j) {
-      compute();
-      __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<(D - 2) * LB>();
-      __builtin_amdgcn_sched_barrier(0);
-      frags((j + 1) % S);
-      issue((j + D) % S, (j + D) * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<(D - 1) * LB>();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-    for (int j = 0; j < KT; ++j) {
-      frags(j % S);
-      issue((j + D) % S, (j + D) * kBK);
-      __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<(D - 1) * LB>();
-      __builtin_amdgcn_sched_barrier(0);
-      compute();
-      __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<(D - 1) * LB>();
-      __builtin_amdgcn_sched_barrier(0);
-    }
   }
-  // No direct-to-LDS load may still be in flight when the workgroup's LDS
-  // is released.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // acc = the tile's products over K steps [k0, k1) (k1 > k0).  Prologue: D
+  // steps in flight, step k0 landed, group 0 holds its first fragments.  The
+  // loop stays branch-free: the last D steps still refill stages that are
+  // never read again, from offsets past k1 (in-range data or range-checked
+  // zeros), and group 0 reads fragments one step past k1 that it never uses.
+  // Returns with every load of this wave landed and every LDS read of the
+  // workgroup done, so the ring may be refilled at once.
+  __device__ __forceinline__ void run(LdsRing& lds, int k0, int k1) {
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[a][b][r] = 0.f;
+    const int n = k1 - k0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, nbytes, 0x00020000);
+#pragma unroll
+    for (int s = 0; s < D; ++s) issue(lds, rs, s, (k0 + s) * kBK);
+    stage_barrier<(D - 1) * LB>();
+    if (grp == 0) frags(lds, 0);
+    stage_barrier<(D - 1) * LB>();
+    // One straight loop per group (the hardware barrier counts arrivals,
+    // not program points; both loops pass the same barriers), so the
+    // fragments stay loop-carried in place.  sched_barrier keeps every MFMA
+    // in its phase.
+    if (grp == 0) {
+      for (int j = 0; j < n; ++j) {
+        compute();
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 2) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+        frags(lds, (j + 1) % S);
+        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      for (int j = 0; j < n; ++j) {
+        frags(lds, j % S);
+        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+        compute();
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 
   // Epilogue.  acc[a][b][e]: x row brow[b] + lane % 16, weight row
-  // arow[a] + 4 * (lane / 16) + e.
-  constexpr int kOutBlocks = NB == 1 ? 8 : 4;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
+  // arow[a] + 4 * (lane / 16) + e.  store_block writes the 4 outputs of one
+  // linear block from v (P5: gate block a, up block a + 4).
+  template <int ACT, bool BIAS>
+  __device__ __forceinline__ void store_block(const GemmArgs& g, int m0, int n0, int a, int b,
+                                              f32x4_t v, f32x4_t u) {
     const int64_t m = (int64_t)m0 + brow[b] + frow;
-    if (m >= g.M) continue;
-    uint16_t* orow = g.out + m * g.ldo;
+    const int64_t n = n0 + (NB == 1 ? arow[a] : wn * 64 + a * 16) + fch * 4;
+    if (m >= g.M || n >= g.N) return;
+    float o[4];
 #pragma unroll
-    for (int a = 0; a < kOutBlocks; ++a) {
-      const int64_t n = n0 + (NB == 1 ? arow[a] : wn * 64 + a * 16) + fch * 4;
-      if (n >= g.N) continue;
-      float o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = acc[a][b][e];
-        if constexpr (NB == 2) {
-          // silu(g) * u with the hardware exp2 / reciprocal (~1 ulp each,
-          // far inside the bf16 output rounding); large |g| saturates
-          // correctly: exp -> inf gives rcp -> 0, exp -> 0 gives rcp -> 1.
-          const float u = acc[a + 4][b][e];
-          const float den = 1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
-          v = v * __builtin_amdgcn_rcpf(den) * u;
-        } else {
-          if constexpr (BIAS) v = v + bf2f(g.bias[n + e]);
-          if constexpr (ACT == UMIC_ACT_GELU) v = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-        }
-        o[e] = v;
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e];
+      if constexpr (NB == 2) {
+        // silu(g) * u with the hardware exp2 / reciprocal (~1 ulp each, far
+        // inside the bf16 output rounding); large |g| saturates correctly:
+        // exp -> inf gives rcp -> 0, exp -> 0 gives rcp -> 1.
+        const float den = 1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+        x = x * __builtin_amdgcn_rcpf(den) * u[e];
+      } else {
+        if constexpr (BIAS) x = x + bf2f(g.bias[n + e]);
+        if constexpr (ACT == UMIC_ACT_GELU) x = 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
       }
-      uint2 pk;
-      pk.x = pack2(o[0], o[1]);
-      pk.y = pack2(o[2], o[3]);
-      *reinterpret_cast<uint2*>(orow + n) = pk;
+      o[e] = x;
+    }
+    uint2 pk;
+    pk.x = pack2(o[0], o[1]);
+    pk.y = pack2(o[2], o[3]);
+    *reinterpret_cast<uint2*>(g.out + m * g.ldo + n) = pk;
+  }
+
+  template <int ACT, bool BIAS>
+  __device__ __forceinline__ void store(const GemmArgs& g, int m0, int n0) {
+    constexpr int kOutBlocks = NB == 1 ? 8 : 4;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int a = 0; a < kOutBlocks; ++a)
+        store_block<ACT, BIAS>(g, m0, n0, a, b, acc[a][b], acc[NB == 2 ? a + 4 : a][b]);
+  }
+};
+
+// Data-parallel: one workgroup per tile, the whole K loop.
+template <int NB, int ACT, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
+  __shared__ LdsRing lds;
+  const int t = xcd_remap(g.tiles);
+  if (t >= g.tiles) return;
+  int m0, n0;
+  tile_origin(g, t, NB == 1 ? kBW : kBW / 2, m0, n0);
+  Pipe<NB> p;
+  p.init(threadIdx.x);
+  p.bind(g, m0, n0);
+  p.run(lds, 0, (int)(g.K / kBK));
+  p.template store<ACT, BIAS>(g, m0, n0);
+}
+
+// Stream-K linear, K-aligned.  With T tiles < G workgroups (one per CU),
+// every workgroup gets the same number of K steps, ks = floor(T*KT / G):
+// T "main" workgroups run K steps [0, ks) of one tile each -- in lockstep,
+// so concurrent tiles share x and weight slabs in L2 exactly as in the
+// data-parallel kernel -- and the other G - T "tail" workgroups split the
+// remaining T x (KT - ks) steps (the [ks, KT) range of every tile, in tile
+// order) evenly between them, stream-K style.  A tile whose K range one
+// workgroup covers is stored directly.  A split tile's segments (the main
+// one, then its tail pieces in K order) are reduced by whichever workgroup
+// arrives last: the others store their fp32 partial in the tile's segment
+// slot and count themselves "written"; the last waits for that count --
+// every workgroup it waits for has already arrived, so it is running and
+// finishes its store without waiting on anything -- then sums the segments
+// in segment order (deterministic whatever the arrival order), applies the
+// epilogue and resets the tile's two counters, so the workspace is
+// all-zero counters again after every launch.
+struct SkArgs {
+  int* counters;   // [2 * T]: arrived, written (zero between launches)
+  f32x4_t* slots;  // [T][kSkMaxSeg][kSlotVec]: segment partials
+  int T, KT, ks;   // tiles, K steps per tile, main steps per tile
+  int G;           // workgroups (T main + G - T tail)
+};
+constexpr int kSlotVec = kBM * kBW / 4;  // f32x4 per partial tile (256 KB)
+constexpr int kSkMaxSeg = 3;             // segments per tile (checked on the host)
+
+// Tail units: v = t * L + r is step ks + r of tile t (L = KT - ks); tail
+// workgroup j owns [j*Ut/Gt, (j+1)*Ut/Gt), Ut = T*L, Gt = G - T (Ut*Gt < 2^31,
+// checked on the host).
+struct SkTail {
+  int L, Ut, Gt;
+  __device__ __forceinline__ explicit SkTail(const SkArgs& s)
+      : L(s.KT - s.ks), Ut(s.T * (s.KT - s.ks)), Gt(s.G - s.T) {}
+  __device__ __forceinline__ int start(int j) const { return j * Ut / Gt; }
+  __device__ __forceinline__ int owner(int v) const { return ((v + 1) * Gt - 1) / Ut; }
+};
+
+template <int ACT, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs s) {
+  __shared__ LdsRing lds;
+  // The arrival order is broadcast through the ring's first word: between
+  // segments the ring is idle (run() returns with every read done and every
+  // load landed) and the next prologue refills it only after two barriers.
+  int* arrival = reinterpret_cast<int*>(&lds[0][0][0]);
+  const int w = xcd_remap(s.G);
+  if (w >= s.G) return;
+  const int tid = threadIdx.x;
+  const SkTail tl(s);
+  Pipe<1> p;
+  // Main workgroup: one segment.  Tail workgroup j: units [v, vend).
+  const bool main_wg = w < s.T;
+  int v = main_wg ? 0 : tl.start(w - s.T);
+  const int vend = main_wg ? 1 : tl.start(w - s.T + 1);
+  while (v < vend) {
+    int t, k0, k1, seg;
+    if (main_wg) {
+      t = w;
+      k0 = 0;
+      k1 = s.ks;
+      seg = 0;
+      v = vend;
+    } else {
+      t = v / tl.L;
+      const int r = v - t * tl.L;
+      const int len = min(tl.L - r, vend - v);
+      k0 = s.ks + r;
+      k1 = k0 + len;
+      seg = 1 + (w - s.T) - tl.owner(t * tl.L);
+      v += len;
+    }
+    int m0, n0;
+    tile_origin(g, t, kBW, m0, n0);
+    // The per-wave invariants (fragment addresses, ...) are derived from an
+    // opaque copy of the thread index, so they are recomputed per segment
+    // instead of staying live (and spilled) across the segment epilogue.
+    int vt = tid;
+    asm volatile("" : "+v"(vt));
+    p.init(vt);
+    p.bind(g, m0, n0);
+    p.run(lds, k0, k1);
+    const int nseg = s.ks == s.KT ? 1
+                                  : 2 + tl.owner(t * tl.L + tl.L - 1) - tl.owner(t * tl.L);
+    if (nseg == 1) {
+      p.template store<ACT, BIAS>(g, m0, n0);
+      continue;
+    }
+    int* arrived = s.counters + 2 * t;
+    int* written = arrived + 1;
+    if (tid == 0)
+      *arrival = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int order = *arrival;
+    __syncthreads();  // the word is refilled by the next segment's loads
+    // Partials move with device-scope relaxed atomic stores and loads (one
+    // dword each, lane-contiguous), so publishing one needs no L2
+    // write-back and reading one no L2 invalidate (either would stall every
+    // CU of the XCD): a partial is visible device-wide once its stores have
+    // completed.  Layout: [segment][block a*4+b][element e][thread].
+    if (order < nseg - 1) {
+      // Not last: publish this segment's partial, then count it.
+      f32x4_t* const dst = reinterpret_cast<f32x4_t*>(s.slots + (int64_t)t * kSkMaxSeg * kSlotVec +
+                                                      (int64_t)seg * kSlotVec) + vt;
+#pragma unroll
+      for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          asm volatile("global_store_dwordx4 %0, %1, off sc1"
+                       :: "v"(dst + (a * 4 + b) * kThreads), "v"(p.acc[a][b]) : "memory");
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) __hip_atomic_fetch_add(written, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+    // Last: wait (device-scope relaxed loads) for the other nseg - 1.
+    if (tid == 0) {
+      while (__hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != nseg - 1)
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __syncthreads();
+    // The (one or two) other segments, in segment order: o1 < o2.
+    const int o1 = seg == 0 ? 1 : 0;
+    const int o2 = seg == 2 ? 1 : 2;
+    const f32x4_t* const tbase =
+        reinterpret_cast<const f32x4_t*>(s.slots + (int64_t)t * kSkMaxSeg * kSlotVec) + vt;
+    const f32x4_t* const src1 = tbase + (int64_t)o1 * kSlotVec;
+    const f32x4_t* const src2 = tbase + (int64_t)o2 * kSlotVec;
+    // One accumulator row (a) at a time: issue its partial loads, wait once
+    // (the wait takes the loaded vectors as operands, so no use moves above
+    // it), sum each block in segment order -- fp32 add is commutative, so
+    // putting this segment's acc in its place gives the segment-order sum --
+    // and store the block at once.
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      f32x4_t q1[4], q2[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        asm volatile("global_load_dwordx4 %0, %1, off sc1"
+                     : "=v"(q1[b]) : "v"(src1 + (a * 4 + b) * kThreads) : "memory");
+      if (nseg == 3) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          asm volatile("global_load_dwordx4 %0, %1, off sc1"
+                       : "=v"(q2[b]) : "v"(src2 + (a * 4 + b) * kThreads) : "memory");
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) q2[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      asm volatile("s_waitcnt vmcnt(0)"
+                   : "+v"(q1[0]), "+v"(q1[1]), "+v"(q1[2]), "+v"(q1[3]),
+                     "+v"(q2[0]), "+v"(q2[1]), "+v"(q2[2]), "+v"(q2[3])
+                   :: "memory");
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const f32x4_t A = p.acc[a][b];
+        f32x4_t r;
+        if (seg == 0) r = A + q1[b];          // s0 = acc, s1
+        else if (seg == 1) r = q1[b] + A;     // s0, s1 = acc
+        else r = q1[b] + q2[b];               // s0, s1 (s2 = acc below)
+        if (nseg == 3) r = seg == 2 ? r + A : r + q2[b];
+        p.template store_block<ACT, BIAS>(g, m0, n0, a, b, r, r);
+      }
+    }
+    if (tid == 0) {
+      __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(written, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -293,6 +507,77 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
   g.tiles = (int)(tm * tn);
   const int64_t grid = ((g.tiles + 7) / 8) * 8;
   hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st, g);
+  return launch_status();
+}
+
+// Stream-K pays when the tiles leave CUs idle and the K loop is long: a
+// split tile costs about 20 us of fixed work (partial stores, the
+// reduction's device-scope loads, extra prologues), measured on MI355X, so
+// the main segment must be at least kSkMinMain steps (q/o at K = 4096 stays
+// data-parallel; down_proj at K = 12288 gains ~10%); every tail workgroup
+// keeps at least kSkMinSteps steps.
+constexpr int kSkMinSteps = 16;
+constexpr int kSkMinMain = 192;
+
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+struct SkPlan {
+  int64_t tiles;
+  int G, KT, ks;
+  int64_t counter_bytes, bytes;
+};
+
+// Workspace layout and grid of the stream-K launch for this shape, or
+// bytes = 0 when the data-parallel kernel is the better (or only) choice.
+// Stream-K needs fewer tiles T than CUs; G = min(CUs, 2T - 1) workgroups,
+// so every tail workgroup covers more than one tile's tail and a tile has
+// at most kSkMaxSeg = 3 segments (main, two tail pieces); every workgroup
+// keeps at least kSkMinSteps steps.
+SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
+  SkPlan pl{0, 0, 0, 0, 0, 0};
+  if (M <= 0 || N <= 0 || K <= 0 || K % kBK) return pl;
+  const int64_t cus = device_cus();
+  const int64_t T = ((M + kBM - 1) / kBM) * ((N + kBW - 1) / kBW);
+  const int64_t KT = K / kBK;
+  const int64_t G = std::min<int64_t>(cus, 2 * T - 1);
+  if (cus <= 0 || G <= T || T * KT * G >= ((int64_t)1 << 31)) return pl;
+  // Main workgroups take a sixth of the tail beyond the even share, which
+  // offsets the tail workgroups' extra segment prologues and partial stores
+  // and makes a main workgroup usually the last to arrive at its tile.
+  const int64_t even = T * KT / G;
+  const int64_t ks = even + (KT - even) / 6;
+  const int64_t L = KT - ks;           // tail steps per tile
+  const int64_t per = T * L / (G - T); // tail steps per tail workgroup, at least
+  if (ks < kSkMinMain || L <= 0 || per < kSkMinSteps) return pl;
+  if (1 + (L + per - 1) / per + 1 > kSkMaxSeg) return pl;
+  pl.tiles = T;
+  pl.G = (int)G;
+  pl.KT = (int)KT;
+  pl.ks = (int)ks;
+  pl.counter_bytes = (2 * T * (int64_t)sizeof(int) + 255) / 256 * 256;
+  pl.bytes = pl.counter_bytes + T * kSkMaxSeg * kSlotVec * (int64_t)sizeof(f32x4_t);
+  return pl;
+}
+
+template <int ACT, bool BIAS>
+int launch_gemm_sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
+  g.tiles_m = (int)((g.M + kBM - 1) / kBM);
+  g.tiles = (int)pl.tiles;
+  SkArgs s{static_cast<int*>(ws),
+           reinterpret_cast<f32x4_t*>(static_cast<char*>(ws) + pl.counter_bytes), (int)pl.tiles,
+           pl.KT, pl.ks, pl.G};
+  const int64_t grid = ((pl.G + 7) / 8) * 8;
+  hipLaunchKernelGGL((gemm_sk_kernel<ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st, g, s);
   return launch_status();
 }
 
@@ -334,6 +619,34 @@ extern "C" int umic_linear_bf16(const void* x, const void* w, const void* bias, 
   if (act == UMIC_ACT_GELU)
     return bias ? launch_gemm<1, UMIC_ACT_GELU, true>(g, st) : launch_gemm<1, UMIC_ACT_GELU, false>(g, st);
   return bias ? launch_gemm<1, UMIC_ACT_NONE, true>(g, st) : launch_gemm<1, UMIC_ACT_NONE, false>(g, st);
+}
+
+extern "C" int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return sk_plan(M, N, K).bytes;
+}
+
+extern "C" int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* out,
+                                   int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                                   int64_t ldo, int act, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0) return UMIC_ERR_INVALID_ARG;
+  const SkPlan pl = sk_plan(M, N, K);
+  if (pl.bytes == 0 || workspace_bytes < pl.bytes || !workspace ||
+      ((uintptr_t)workspace & 255u))  // data-parallel path
+    return umic_linear_bf16(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, stream);
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU) return UMIC_ERR_INVALID_ARG;
+  if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
+  if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
+  if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
+  GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
+             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0};
+  hipStream_t st = as_stream(stream);
+  if (act == UMIC_ACT_GELU)
+    return bias ? launch_gemm_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
+                : launch_gemm_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
+  return bias ? launch_gemm_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
+              : launch_gemm_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
 }
 
 extern "C" int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void* wu, void* out,

@@ -43,9 +43,16 @@ SIGNATURES: dict[str, list] = {
                          + [_I64] * 2 + [_P],
     "umic_linear_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "umic_gate_silu_mul_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "umic_linear_workspace_bytes": [_I64, _I64, _I64],
+    "umic_linear_ws_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
     "umic_version": [],
     "umic_error_string": [_I],
 }
+
+
+# Return types other than int.
+RESTYPES = {"umic_version": ctypes.c_char_p, "umic_error_string": ctypes.c_char_p,
+            "umic_linear_workspace_bytes": _I64}
 
 
 class UmicLibraryError(RuntimeError):
@@ -81,7 +88,7 @@ def load(path: str | None = None) -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_char_p if name in ("umic_version", "umic_error_string") else _I
+            fn.restype = RESTYPES.get(name, _I)
         _lib = lib
         HAS_KERNELS = True
         return lib

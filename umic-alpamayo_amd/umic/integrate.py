@@ -41,6 +41,14 @@ FUSE_MIN_ROWS = 64
 # Projection sites routed to the fused linear (reference integrate.py:91).
 INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
 
+# Per-site choice for the P5 MLP's down_proj, which the reference leaves on
+# the vendor BLAS (integrate.py:80-90, measured a loser on Thor): on MI355X
+# this library's stream-K linear beats hipBLASLt where it applies (fewer
+# output tiles than CUs and a long K loop: at M=3100, K=12288 it ran in
+# 278 us vs 298 us), so the fused MLP uses it for exactly those shapes and
+# the vendor module for every other one.
+DOWN_PROJ_STREAM_K = True
+
 # ViT projection site list kept from the reference (integrate.py:95); not
 # used by apply().
 VIT_LINEAR_NAMES = ("qkv",)
@@ -85,7 +93,12 @@ def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
     # takes -- the kernel reads the original weight memory.
     h = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
-    return self.down_proj(h)
+    down = self.down_proj
+    if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear)
+            and linear.linear_eligible(h, down.weight, down.bias)
+            and linear.stream_k_planned(h, down.weight)):
+        return linear.linear_hip(h, down.weight, down.bias)
+    return down(h)
 
 
 def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:

@@ -65,11 +65,43 @@ def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
     N = w.shape[0]
     out = torch.empty((M, N), dtype=x.dtype, device=x.device)
     with _lib.device_of(x):
-        _lib.call("umic_linear_bf16", x2d.data_ptr(), w.data_ptr(), _lib.ptr(b), out.data_ptr(),
+        stream = _lib.stream_of(x)
+        ws, ws_bytes = workspace(x.device, stream, M, N, K)
+        _lib.call("umic_linear_ws_bf16", x2d.data_ptr(), w.data_ptr(), _lib.ptr(b), out.data_ptr(),
                   M, N, K, ld(x2d), ld(w), N,
                   _lib.UMIC_ACT_GELU if act == "gelu" else _lib.UMIC_ACT_NONE,
-                  _lib.stream_of(x))
+                  _lib.ptr(ws), ws_bytes, stream)
     return out.reshape(*shape[:-1], N)
+
+
+def stream_k_planned(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """True if linear_hip(x, weight) runs the stream-K schedule on this device."""
+    if not x.is_cuda:
+        return False
+    M = x.numel() // x.shape[-1] if x.shape[-1] else 0
+    N, K = weight.shape
+    with _lib.device_of(x):
+        return _lib.lib().umic_linear_workspace_bytes(M, N, K) > 0
+
+
+# Stream-K workspaces, one per (device, stream): the kernel leaves its
+# counters at zero after every launch, so a workspace is zeroed once, when it
+# is created, and reused by every later call on that stream (calls on one
+# stream never overlap).
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, stream: int, M: int, N: int, K: int):
+    """(tensor, bytes) the stream-K linear needs for this shape, or (None, 0)."""
+    need = _lib.lib().umic_linear_workspace_bytes(M, N, K)
+    if need <= 0:
+        return None, 0
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws, ws.numel()
 
 
 # Name of the reference's wrapper (src/umic/kernels/linear.py:118).
