@@ -272,6 +272,47 @@ def copy_ceiling() -> int:
     return 0
 
 
+def vit_sites() -> int:
+    """The ViT projection sites the reference left on the vendor library
+    (src/umic/integrate.py:93-95, 261-319), this library's linear against
+    hipBLASLt at M=16384 tokens, hidden 1280: one JSON line per site."""
+    import torch
+
+    from umic import _lib
+    from umic.kernels import linear
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    F = torch.nn.functional
+
+    def timed(fn, reps=30):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    M = 16384
+    for site, K, N, act in (("qkv", 1280, 3840, None), ("fc1_gelu", 1280, 5120, "gelu"),
+                            ("fc2", 5120, 1280, None)):
+        x = _bf(M, K)
+        w, b = _bf(N, K, scale=0.02), _bf(N, scale=0.1)
+        ours = timed(lambda: linear.linear_hip(x, w, b, act=act))
+        if act:
+            vendor = timed(lambda: F.gelu(F.linear(x, w, b)))
+        else:
+            vendor = timed(lambda: F.linear(x, w, b))
+        print(json.dumps({"site": site, "M": M, "K": K, "N": N, "act": act,
+                          "umic_us": round(ours, 1), "vendor_us": round(vendor, 1),
+                          "umic_tflops": round(2 * M * N * K / ours / 1e6, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -283,6 +324,8 @@ def main() -> int:
                     help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain device copies of the norm/RoPE byte counts")
+    ap.add_argument("--vit-sites", action="store_true",
+                    help="time the ViT projection sites, this library against hipBLASLt")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -294,6 +337,8 @@ def main() -> int:
         return pmc_probe()
     if args.copy_ceiling:
         return copy_ceiling()
+    if args.vit_sites:
+        return vit_sites()
 
     import torch
 

@@ -223,8 +223,10 @@ struct Pipe {
   // loop stays branch-free: the last D steps still refill stages that are
   // never read again, from offsets past k1 (in-range data or range-checked
   // zeros), and group 0 reads fragments one step past k1 that it never uses.
-  // Returns with every load of this wave landed and every LDS read of the
-  // workgroup done, so the ring may be refilled at once.
+  // Returns with every load of every wave landed and every LDS read done:
+  // the last steps' refills land asynchronously, and each wave's
+  // s_waitcnt covers only its own, so a barrier follows before anyone
+  // writes the ring (staged output, the arrival word, the next prologue).
   __device__ __forceinline__ void run(LdsRing& lds, int k0, int k1) {
 #pragma unroll
     for (int a = 0; a < 8; ++a)
@@ -269,18 +271,49 @@ struct Pipe {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    stage_barrier<0>();
   }
 
   // Epilogue.  acc[a][b][e]: x row brow[b] + lane % 16, weight row
-  // arow[a] + 4 * (lane / 16) + e.  store_block writes the 4 outputs of one
-  // linear block from v (P5: gate block a, up block a + 4).
+  // arow[a] + 4 * (lane / 16) + e.  The output tile is staged in LDS (the
+  // ring is idle once run() has returned) as row-major bf16 rows padded by
+  // 16 bytes, then streamed to HBM as whole rows with 16-byte stores: stored
+  // straight from the fragment layout, each store instruction would touch
+  // 16 rows (16 partial cache lines), which measured ~7 us per tile against
+  // ~1 us this way.
+  static constexpr int kOutCols = NB == 1 ? kBW : kBW / 2;  // output columns per tile
+  static constexpr int kOutRow = kOutCols * 2 + 16;         // staged bytes per row
+  static_assert(kBM * kOutRow <= (int)sizeof(LdsRing), "staged tile must fit the ring");
+
+  __device__ __forceinline__ int out_col(int a) const {
+    return (NB == 1 ? arow[a] : wn * 64 + a * 16) + fch * 4;
+  }
+
+  // Bias of this lane's 4 output columns of column block a: 4 consecutive
+  // bf16, 8-byte aligned (bias and N are multiples of 4 elements); columns
+  // past N are never written out.
+  template <bool BIAS>
+  __device__ __forceinline__ f32x4_t load_bias(const GemmArgs& g, int n0, int a) const {
+    f32x4_t bias = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (NB == 1 && BIAS) {
+      if (n0 + out_col(a) < g.N) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(g.bias + n0 + out_col(a));
+        bias[0] = bf_lo(bw.x);
+        bias[1] = bf_hi(bw.x);
+        bias[2] = bf_lo(bw.y);
+        bias[3] = bf_hi(bw.y);
+      }
+    }
+    return bias;
+  }
+
+  // Block (a, b) of the tile from fp32 v (P5: gate v, up u): bias, GELU or
+  // silu(g)*u, one bf16 rounding, into the staged tile.
   template <int ACT, bool BIAS>
-  __device__ __forceinline__ void store_block(const GemmArgs& g, int m0, int n0, int a, int b,
-                                              f32x4_t v, f32x4_t u) {
-    const int64_t m = (int64_t)m0 + brow[b] + frow;
-    const int64_t n = n0 + (NB == 1 ? arow[a] : wn * 64 + a * 16) + fch * 4;
-    if (m >= g.M || n >= g.N) return;
+  __device__ __forceinline__ void stage_block(LdsRing& lds, int a, int b, f32x4_t v, f32x4_t u,
+                                              f32x4_t bias) {
+    const int row = brow[b] + frow;
+    const int col = out_col(a);
     float o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -292,7 +325,7 @@ struct Pipe {
         const float den = 1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
         x = x * __builtin_amdgcn_rcpf(den) * u[e];
       } else {
-        if constexpr (BIAS) x = x + bf2f(g.bias[n + e]);
+        if constexpr (BIAS) x = x + bias[e];
         if constexpr (ACT == UMIC_ACT_GELU) x = 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
       }
       o[e] = x;
@@ -300,17 +333,42 @@ struct Pipe {
     uint2 pk;
     pk.x = pack2(o[0], o[1]);
     pk.y = pack2(o[2], o[3]);
-    *reinterpret_cast<uint2*>(g.out + m * g.ldo + n) = pk;
+    *reinterpret_cast<uint2*>(reinterpret_cast<char*>(&lds[0][0][0]) + row * kOutRow + col * 2) = pk;
+  }
+
+  // Stream the staged tile to out[m0.., n0..]: each thread moves 16-byte
+  // chunks, a wavefront whole contiguous rows.  Barriers on both sides: the
+  // tile must be complete, and the ring may be refilled afterwards.
+  __device__ __forceinline__ void flush(LdsRing& lds, const GemmArgs& g, int m0, int n0) {
+    __syncthreads();
+    constexpr int kChunks = kOutCols / 8;  // 16-byte chunks per row
+    constexpr int kRowsPerPass = kThreads / kChunks;
+    const int c = threadIdx.x % kChunks;
+    const int64_t n = n0 + c * 8;
+    const char* base = reinterpret_cast<const char*>(&lds[0][0][0]);
+    if (n < g.N) {
+#pragma unroll 4
+      for (int r = threadIdx.x / kChunks; r < kBM; r += kRowsPerPass) {
+        const int64_t m = (int64_t)m0 + r;
+        if (m >= g.M) break;
+        *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n) =
+            *reinterpret_cast<const u32x4*>(base + r * kOutRow + c * 16);
+      }
+    }
+    __syncthreads();
   }
 
   template <int ACT, bool BIAS>
-  __device__ __forceinline__ void store(const GemmArgs& g, int m0, int n0) {
+  __device__ __forceinline__ void store(LdsRing& lds, const GemmArgs& g, int m0, int n0) {
     constexpr int kOutBlocks = NB == 1 ? 8 : 4;
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int a = 0; a < kOutBlocks; ++a) {
+      const f32x4_t bias = load_bias<BIAS>(g, n0, a);
 #pragma unroll
-      for (int a = 0; a < kOutBlocks; ++a)
-        store_block<ACT, BIAS>(g, m0, n0, a, b, acc[a][b], acc[NB == 2 ? a + 4 : a][b]);
+      for (int b = 0; b < 4; ++b)
+        stage_block<ACT, BIAS>(lds, a, b, acc[a][b], acc[NB == 2 ? a + 4 : a][b], bias);
+    }
+    flush(lds, g, m0, n0);
   }
 };
 
@@ -326,7 +384,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   p.init(threadIdx.x);
   p.bind(g, m0, n0);
   p.run(lds, 0, (int)(g.K / kBK));
-  p.template store<ACT, BIAS>(g, m0, n0);
+  p.template store<ACT, BIAS>(lds, g, m0, n0);
 }
 
 // Stream-K linear, K-aligned.  With T tiles < G workgroups (one per CU),
@@ -411,7 +469,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
     const int nseg = s.ks == s.KT ? 1
                                   : 2 + tl.owner(t * tl.L + tl.L - 1) - tl.owner(t * tl.L);
     if (nseg == 1) {
-      p.template store<ACT, BIAS>(g, m0, n0);
+      p.template store<ACT, BIAS>(lds, g, m0, n0);
       continue;
     }
     int* arrived = s.counters + 2 * t;
@@ -461,6 +519,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
     // and store the block at once.
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
+      const f32x4_t bias = p.template load_bias<BIAS>(g, n0, a);
       f32x4_t q1[4], q2[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b)
@@ -487,9 +546,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
         else if (seg == 1) r = q1[b] + A;     // s0, s1 = acc
         else r = q1[b] + q2[b];               // s0, s1 (s2 = acc below)
         if (nseg == 3) r = seg == 2 ? r + A : r + q2[b];
-        p.template store_block<ACT, BIAS>(g, m0, n0, a, b, r, r);
+        p.template stage_block<ACT, BIAS>(lds, a, b, r, r, bias);
       }
     }
+    p.flush(lds, g, m0, n0);
     if (tid == 0) {
       __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(written, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
