@@ -33,6 +33,9 @@ six fused norm/RoPE kernels (algorithmic bytes / summed durations);
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
 (by time) of the step; cpu_baseline = the CPU oracle (scalar C, one core)
 timed on a bounded sample of the same norm/RoPE workload, in GB/s.
+layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
+prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
+HIP graph); --no-layer skips it.
 """
 
 from __future__ import annotations
@@ -272,6 +275,80 @@ def copy_ceiling() -> int:
     return 0
 
 
+def layer_step() -> dict:
+    """one Qwen3-VL text decoder layer (hidden 4096, 32 q /
+    8 kv heads, head_dim 128, intermediate 12288, random N(0, 0.02) weights,
+    norms 1 + N(0, 0.1)) timed eager and with the fused path injected
+    (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope):
+    prefill at M=3100 and decode at M=1, the decode step also captured in a
+    HIP graph (torch.cuda.CUDAGraph) and replayed, as the reference's decode
+    runner does (src/umic/graph.py:155-167)."""
+    import torch
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextDecoderLayer,
+                                                                Qwen3VLTextRotaryEmbedding)
+
+    from umic import integrate
+
+    cfg = Qwen3VLTextConfig(hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                            num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                            rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+                            attn_implementation="sdpa")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    layer = Qwen3VLTextDecoderLayer(cfg, 0).to(torch.bfloat16).to("cuda").eval()
+    with torch.no_grad():
+        for name, prm in layer.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                prm.copy_(1 + 0.1 * torch.randn(prm.shape, generator=gen, device="cuda"))
+            else:
+                prm.copy_(0.02 * torch.randn(prm.shape, generator=gen, device="cuda"))
+    rot = Qwen3VLTextRotaryEmbedding(cfg).to("cuda")
+    inputs = {}
+    for M in (3100, 1):
+        h = _bf(1, M, 4096, gen=gen)
+        inputs[M] = (h, rot(h, torch.arange(M, device="cuda")[None]))
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3  # us
+
+    res = {}
+    with torch.no_grad():
+        run = {M: (lambda h=h, cs=cs: layer(h, position_embeddings=cs))
+               for M, (h, cs) in inputs.items()}
+        res["prefill_M3100_eager_ms"] = round(timed(run[3100], 10) / 1e3, 4)
+        res["decode_M1_eager_us"] = round(timed(run[1], 200), 1)
+        integrate.fuse_mlps(layer)
+        integrate.fuse_linears(layer)
+        integrate.fuse_rmsnorms(layer)
+        integrate.fuse_add_rmsnorm(layer)
+        integrate.fuse_text_rope()
+        try:
+            res["prefill_M3100_umic_ms"] = round(timed(run[3100], 10) / 1e3, 4)
+            res["decode_M1_umic_us"] = round(timed(run[1], 200), 1)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                run[1]()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run[1]()
+            res["decode_M1_umic_graph_us"] = round(timed(graph.replay, 200), 1)
+        finally:
+            integrate.unfuse_mlps(layer)
+            integrate.unfuse_rope()
+    return res
+
+
 def vit_sites() -> int:
     """The ViT projection sites the reference left on the vendor library
     (src/umic/integrate.py:93-95, 261-319), this library's linear against
@@ -326,6 +403,8 @@ def main() -> int:
                     help="time plain device copies of the norm/RoPE byte counts")
     ap.add_argument("--vit-sites", action="store_true",
                     help="time the ViT projection sites, this library against hipBLASLt")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="skip the decoder-layer (config 5) prefill/decode timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -405,7 +484,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(sum(k["us"] for k in kern.values()) / 1e3, 3),
+        "ms_per_step": round(sum(v["us"] for n, v in kern.items() if n != "down_proj_vendor")
+                             / 1e3, 3),
         "wall_ms_per_step": round(wall / K * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
@@ -414,12 +494,14 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "BASELINE configs 2-4 at full size: norms [3100,4096] and "
                                "[16384,1280], RoPE text q/k [1,32|8,3100,128] and vision "
-                               "[16384,16,80], q/o proj and P5 MLP at M=3100 K=4096 N=4096|12288",
+                               "[16384,16,80], q/o proj and P5 MLP at M=3100 K=4096 N=4096|12288, "
+                               "down_proj K=12288 N=4096",
                    "rows_lm": 3100, "rows_vit": 16384, "input_rings": rings},
         "hbm_frac": round(agg / HBM_PEAK_GBS, 4),
         "mlp_prefill_ms": round(mlp_ms, 4),
         "kernels": kern,
         "roofline": roof,
+        "layer": None if args.no_layer else layer_step(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_s),
     }
     print(json.dumps(out), flush=True)
