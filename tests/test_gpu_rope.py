@@ -83,6 +83,29 @@ def test_text_rope_contiguous_and_batched():
     assert torch.equal(qo1, rq1) and torch.equal(ko1, rk1)
 
 
+def test_text_rope_unaligned_tables_take_the_staged_path():
+    """bf16 tables are read per item with 16-byte loads when their bases and
+    row strides allow it; tables at an odd element offset (2-byte aligned
+    rows) are staged through LDS instead -- same results either way."""
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
+
+    g = torch.Generator().manual_seed(2)
+    S, Hq, Hk, D = 300, 8, 2, 128
+    cos, sin = text_tables(S, D, 1e6)
+    q = bf16_randn(1, S, Hq, D, gen=g).to(DEV).transpose(1, 2)
+    k = bf16_randn(1, S, Hk, D, gen=g).to(DEV).transpose(1, 2)
+    for shift in (0, 1):
+        cbig = torch.zeros(1, S, D + 8, dtype=torch.bfloat16, device=DEV)
+        sbig = torch.zeros_like(cbig)
+        cbig[..., shift:shift + D] = cos.to(DEV)
+        sbig[..., shift:shift + D] = sin.to(DEV)
+        c, s_ = cbig[..., shift:shift + D], sbig[..., shift:shift + D]
+        assert (c.data_ptr() % 16 == 0) == (shift == 0)
+        qo, ko = rope.apply_rotary_text_hip(q, k, c, s_)
+        rq, rk = apply_rotary_pos_emb(q, k, cos.to(DEV), sin.to(DEV))
+        assert torch.equal(qo, rq) and torch.equal(ko, rk), shift
+
+
 @pytest.mark.parametrize("grid,H", [([[1, 32, 32]] * 16, 16), ([[1, 4, 6], [1, 6, 4]], 3),
                                     ([[2, 4, 4]], 1)])
 def test_vision_rope_packed_qkv(grid, H):

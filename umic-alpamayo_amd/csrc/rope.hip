@@ -9,12 +9,17 @@
 // head, then the heads of a position, so each load/store instruction of a
 // wavefront covers whole contiguous head rows of q (then k).
 //
-// One block serves a flat range of 1024 items (4 per thread, all loads in
-// flight together): the cos/sin rows of the positions it touches are staged
-// once into LDS -- read from HBM once for q AND k, where the reference's
-// per-tensor launches read them twice -- and every item is rotated from
-// registers.  Activations are streamed with
-// non-temporal loads/stores: each element is read once and written once.
+// Tables.  cos/sin are read once from HBM for q AND k (the reference's
+// per-tensor launches read them twice).  fp32 tables (vision) are staged
+// into LDS per block: one block serves a flat range of 1024 items (4 per
+// thread, all loads in flight together), stages the cos/sin rows of the
+// positions it touches, and rotates every item from registers.  bf16 tables
+// (text, [S, 128] = 0.8 MB each, L2-resident) are instead read per item
+// straight from global -- 16 bytes per half, the same width as the item --
+// with 512 items per block: measured 8% faster than staging (no staging
+// loop, no barrier), while for fp32 tables the per-item reads would be 4x
+// the item's own bytes and staging wins.  Activations are streamed with
+// non-temporal loads: each element is read once and written once.
 //
 // Arithmetic modes (no fp contraction anywhere in this library):
 //   TEXT   -- every op rounds to bf16, as the eager bf16 chain does:
@@ -76,6 +81,19 @@ struct Chunk<1> {
     *p = (uint16_t)f2bf(f[0]);
   }
 };
+
+// 8 consecutive table values (fp32 or bf16) at element offset off.
+template <bool CS32>
+__device__ __forceinline__ void load_cs8(const void* base, int64_t off, float f[8]) {
+  if constexpr (CS32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+    const float4 lo = p[0], hi = p[1];
+    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  } else {
+    unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off), f);
+  }
+}
 
 template <int MODE, int VEC>
 __device__ __forceinline__ void rotate(const float* xl, const float* xh, const float* cl,
@@ -191,8 +209,72 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
   }
 }
 
+// bf16 tables, 16-byte chunks: cos/sin read per item from global (see the
+// header).  kDirectItems items per thread, all q/k loads issued first.
+constexpr int kDirectItems = 2;
+template <int MODE>
+__global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
+  constexpr int VEC = 8;
+  const int64_t npos = a.B * a.S;
+  const int D = (int)a.D;
+  const int half = D / 2;
+  const int C = half / VEC;
+  const int ipp = (int)(a.Hq + a.Hk) * C;
+  const int nq = (int)a.Hq * C;
+  const int64_t nitems = npos * ipp;
+  const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const uint16_t* xs[kDirectItems];
+  uint16_t* os[kDirectItems];
+  int64_t cso[kDirectItems];
+  int dls[kDirectItems];
+  bool ok[kDirectItems];
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    int64_t it = base + u * 256 + (int)threadIdx.x;
+    ok[u] = it < nitems;
+    if (!ok[u]) it = 0;  // re-reads item 0 (always valid) and stores nothing
+    const int64_t p = it / ipp;
+    const int j = (int)(it - p * ipp);
+    int64_t b = 0, sidx = p;
+    if (a.B != 1) {
+      b = p / a.S;
+      sidx = p - b * a.S;
+    }
+    const bool isq = j < nq;
+    const int jj = isq ? j : j - nq;
+    const int h = jj / C, c = jj - h * C;
+    if (isq) {
+      xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
+      os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
+    } else {
+      xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
+      os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
+    }
+    dls[u] = c * VEC;
+    cso[u] = b * a.cs_sb + sidx * a.cs_ss;
+  }
+  float xl[kDirectItems][VEC], xh[kDirectItems][VEC];
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    Chunk<VEC>::load(xs[u] + dls[u], xl[u]);
+    Chunk<VEC>::load(xs[u] + half + dls[u], xh[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    if (!ok[u]) continue;
+    float cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
+    load_cs8<false>(a.cos, cso[u] + dls[u], cl);
+    load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
+    load_cs8<false>(a.sin, cso[u] + dls[u], sl);
+    load_cs8<false>(a.sin, cso[u] + half + dls[u], sh);
+    rotate<MODE, VEC>(xl[u], xh[u], cl, ch, sl, sh, ol, oh);
+    Chunk<VEC>::store(os[u] + dls[u], ol);
+    Chunk<VEC>::store(os[u] + half + dls[u], oh);
+  }
+}
+
 template <int MODE, bool CS32, int VEC>
-int launch_rope(const RopeArgs& a, hipStream_t st) {
+int launch_staged(const RopeArgs& a, hipStream_t st) {
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
   // kItems items per thread in one pass; the positions a range touches
@@ -208,11 +290,27 @@ int launch_rope(const RopeArgs& a, hipStream_t st) {
   return launch_status();
 }
 
+// direct_ok: the bf16 tables allow 16-byte reads (aligned bases, row
+// strides multiples of 8 elements); otherwise they are staged.
+template <int MODE, bool CS32, int VEC>
+int launch_rope(const RopeArgs& a, bool direct_ok, hipStream_t st) {
+  if constexpr (!CS32 && VEC == 8) {
+    if (!direct_ok) return launch_staged<MODE, CS32, VEC>(a, st);
+    const int64_t nitems = a.B * a.S * (a.Hq + a.Hk) * (a.D / 2 / VEC);
+    const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+    if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((rope_qk_direct_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return launch_status();
+  } else {
+    return launch_staged<MODE, CS32, VEC>(a, st);
+  }
+}
+
 template <int MODE, bool CS32>
-int dispatch_vec(const RopeArgs& a, int vec, hipStream_t st) {
-  if (vec == 8) return launch_rope<MODE, CS32, 8>(a, st);
-  if (vec == 2) return launch_rope<MODE, CS32, 2>(a, st);
-  return launch_rope<MODE, CS32, 1>(a, st);
+int dispatch_vec(const RopeArgs& a, int vec, bool direct_ok, hipStream_t st) {
+  if (vec == 8) return launch_rope<MODE, CS32, 8>(a, direct_ok, st);
+  if (vec == 2) return launch_staged<MODE, CS32, 2>(a, st);
+  return launch_staged<MODE, CS32, 1>(a, st);
 }
 
 }  // namespace
@@ -263,8 +361,10 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   const int vec = (all_mult(8) && all_aligned(16)) ? 8 : (all_mult(2) && all_aligned(4)) ? 2 : 1;
   if (vec == 1 && !all_aligned(2)) return UMIC_ERR_UNSUPPORTED;
 
+  const bool direct_ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
+                         (uintptr_t)sin % 16 == 0;
   hipStream_t st = as_stream(stream);
-  if (mode == UMIC_ROPE_TEXT) return dispatch_vec<UMIC_ROPE_TEXT, false>(a, vec, st);
-  if (cs_fp32) return dispatch_vec<UMIC_ROPE_VISION, true>(a, vec, st);
-  return dispatch_vec<UMIC_ROPE_VISION, false>(a, vec, st);
+  if (mode == UMIC_ROPE_TEXT) return dispatch_vec<UMIC_ROPE_TEXT, false>(a, vec, direct_ok, st);
+  if (cs_fp32) return dispatch_vec<UMIC_ROPE_VISION, true>(a, vec, direct_ok, st);
+  return dispatch_vec<UMIC_ROPE_VISION, false>(a, vec, direct_ok, st);
 }
