@@ -423,6 +423,44 @@ struct SkTail {
   __device__ __forceinline__ int owner(int v) const { return ((v + 1) * Gt - 1) / Ut; }
 };
 
+// Device-scope (sc1) 16-byte loads of one accumulator row's partials,
+// p[b * kThreads] for b = 0..3, issued and waited for inside ONE asm
+// statement: the outputs are valid when it returns.  (A load left in flight
+// across statements is unsafe: the compiler may move or spill its destination
+// register before the data arrives.)  Early-clobber outputs keep the
+// destinations off the address registers.
+__device__ __forceinline__ void load_row_sc1(f32x4_t (&q)[4], const f32x4_t* p) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+      : "v"(p), "v"(p + kThreads), "v"(p + 2 * kThreads), "v"(p + 3 * kThreads)
+      : "memory");
+}
+
+// The same for two segments' rows at once (eight loads, one wait).
+__device__ __forceinline__ void load_row_sc1(f32x4_t (&q)[4], f32x4_t (&r)[4],
+                                             const f32x4_t* p, const f32x4_t* u) {
+  asm volatile(
+      "global_load_dwordx4 %0, %8, off sc1\n\t"
+      "global_load_dwordx4 %1, %9, off sc1\n\t"
+      "global_load_dwordx4 %2, %10, off sc1\n\t"
+      "global_load_dwordx4 %3, %11, off sc1\n\t"
+      "global_load_dwordx4 %4, %12, off sc1\n\t"
+      "global_load_dwordx4 %5, %13, off sc1\n\t"
+      "global_load_dwordx4 %6, %14, off sc1\n\t"
+      "global_load_dwordx4 %7, %15, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]),
+        "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(p), "v"(p + kThreads), "v"(p + 2 * kThreads), "v"(p + 3 * kThreads),
+        "v"(u), "v"(u + kThreads), "v"(u + 2 * kThreads), "v"(u + 3 * kThreads)
+      : "memory");
+}
+
 template <int ACT, bool BIAS>
 __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs s) {
   __shared__ LdsRing lds;
@@ -512,32 +550,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
         reinterpret_cast<const f32x4_t*>(s.slots + (int64_t)t * kSkMaxSeg * kSlotVec) + vt;
     const f32x4_t* const src1 = tbase + (int64_t)o1 * kSlotVec;
     const f32x4_t* const src2 = tbase + (int64_t)o2 * kSlotVec;
-    // One accumulator row (a) at a time: issue its partial loads, wait once
-    // (the wait takes the loaded vectors as operands, so no use moves above
-    // it), sum each block in segment order -- fp32 add is commutative, so
-    // putting this segment's acc in its place gives the segment-order sum --
-    // and store the block at once.
+    // One accumulator row (a) at a time: load its partials (loads and wait in
+    // one asm statement, so its outputs are complete when it returns), sum
+    // each block in segment order -- fp32 add is commutative, so putting this
+    // segment's acc in its place gives the segment-order sum -- and stage the
+    // block at once.
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
       const f32x4_t bias = p.template load_bias<BIAS>(g, n0, a);
       f32x4_t q1[4], q2[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        asm volatile("global_load_dwordx4 %0, %1, off sc1"
-                     : "=v"(q1[b]) : "v"(src1 + (a * 4 + b) * kThreads) : "memory");
       if (nseg == 3) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          asm volatile("global_load_dwordx4 %0, %1, off sc1"
-                       : "=v"(q2[b]) : "v"(src2 + (a * 4 + b) * kThreads) : "memory");
+        load_row_sc1(q1, q2, src1 + a * 4 * kThreads, src2 + a * 4 * kThreads);
       } else {
+        load_row_sc1(q1, src1 + a * 4 * kThreads);
 #pragma unroll
         for (int b = 0; b < 4; ++b) q2[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
-      asm volatile("s_waitcnt vmcnt(0)"
-                   : "+v"(q1[0]), "+v"(q1[1]), "+v"(q1[2]), "+v"(q1[3]),
-                     "+v"(q2[0]), "+v"(q2[1]), "+v"(q2[2]), "+v"(q2[3])
-                   :: "memory");
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const f32x4_t A = p.acc[a][b];
