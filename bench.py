@@ -35,7 +35,9 @@ mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
 timed on a bounded sample of the same norm/RoPE workload, in GB/s.
 layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
 prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
-HIP graph); --no-layer skips it.
+HIP graph); --no-layer skips it.  kv_cache = text RoPE fused with the
+in-place KV-cache append against RoPE + two slice copies, at prefill and at a
+32-token flow step; --no-kv-cache skips it.
 """
 
 from __future__ import annotations
@@ -349,6 +351,81 @@ def layer_step() -> dict:
     return res
 
 
+def kv_cache_step(reps: int = 20) -> dict:
+    """Text RoPE fused with the in-place KV-cache append
+    (umic_rope_kv_append_bf16) against the chain it replaces -- this
+    library's q+k RoPE, then the cache's two slice assignments
+    (src/umic/cache.py:69-70) -- at BASELINE config 5 head counts (32 q /
+    8 kv heads, head_dim 128): a 3100-token prefill into an empty cache and a
+    32-token flow step appended after a 3094-token prefix.  Inputs and caches
+    rotate over rings of >= 640 MB so no launch is served from the Infinity
+    Cache.  Algorithmic bytes: q, k, v read and written once, cos/sin read
+    once: 2*2*(Hq+2*Hk)*S*D + 2*2*S*D."""
+    import torch
+
+    from umic.kernels import rope
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    Hq, Hk, D, L = 32, 8, 128, 3200
+    sa, sb = _bf(8192, 8192, gen=gen), _bf(8192, 8192, gen=gen)  # spacer GEMM operands
+    res = {}
+    for tag, S, pos in (("prefill_S3100", 3100, 0), ("flow_S32", 32, 3094)):
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        ang = torch.arange(pos, pos + S, dtype=torch.float32)[:, None] * inv[None]
+        emb = torch.cat((ang, ang), -1)
+        cos, sin = (f(emb).to(torch.bfloat16)[None].cuda() for f in (torch.cos, torch.sin))
+        per_set = 2 * (Hq + 2 * Hk) * S * D + 2 * 2 * Hk * L * D
+        n = max(2, min(32, int(-(-640e6 // per_set))))
+        sets = [tuple(_bf(1, S, H, D, gen=gen).transpose(1, 2) for H in (Hq, Hk, Hk))
+                + (torch.empty(1, Hk, L, D, dtype=torch.bfloat16, device="cuda"),
+                   torch.empty(1, Hk, L, D, dtype=torch.bfloat16, device="cuda"))
+                for _ in range(n)]
+
+        def fused(i):
+            q, k, v, kc, vc = sets[i % n]
+            return rope.rope_kv_append(q, k, v, cos, sin, kc, vc, pos)
+
+        def unfused(i):
+            q, k, v, kc, vc = sets[i % n]
+            qo, ko = rope.apply_rotary_text_hip(q, k, cos, sin)
+            kc[:, :, pos:pos + S] = ko
+            vc[:, :, pos:pos + S] = v
+            return qo
+
+        def timed(fn):
+            """(GPU us per call, host us per call).  GPU time: the calls are
+            queued behind ~2 ms of spacer GEMMs, so the events see device
+            time only; host time: wall clock of back-to-back calls."""
+            for i in range(3):
+                fn(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            keep = [None] * n
+            for _ in range(2):
+                torch.matmul(sa, sb)
+            e0.record()
+            for i in range(reps):
+                keep[i % n] = fn(i)
+            e1.record()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(reps):
+                keep[i % n] = fn(i)
+            host = (time.perf_counter() - t0) / reps * 1e6
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / reps * 1e3, host
+
+        nbytes = 2 * 2 * (Hq + 2 * Hk) * S * D + 2 * 2 * S * D
+        (us_f, host_f), (us_u, host_u) = timed(fused), timed(unfused)
+        res[tag] = {"fused_us": round(us_f, 2), "unfused_us": round(us_u, 2),
+                    "fused_host_us": round(host_f, 1), "unfused_host_us": round(host_u, 1),
+                    "bytes": nbytes, "gbps": round(nbytes / (us_f * 1e-6) / 1e9, 1),
+                    "frac": round(nbytes / (us_f * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "ring": n}
+        del sets
+    return res
+
+
 def vit_sites() -> int:
     """The ViT projection sites the reference left on the vendor library
     (src/umic/integrate.py:93-95, 261-319), this library's linear against
@@ -405,6 +482,8 @@ def main() -> int:
                     help="time the ViT projection sites, this library against hipBLASLt")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the decoder-layer (config 5) prefill/decode timing")
+    ap.add_argument("--no-kv-cache", action="store_true",
+                    help="skip the fused RoPE + KV-cache append timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -502,6 +581,7 @@ def main() -> int:
         "kernels": kern,
         "roofline": roof,
         "layer": None if args.no_layer else layer_step(),
+        "kv_cache": None if args.no_kv_cache else kv_cache_step(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_s),
     }
     print(json.dumps(out), flush=True)

@@ -116,6 +116,39 @@ int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void* k_out,
                       int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
                       int64_t cs_sb, int64_t cs_ss, void* stream);
 
+/*
+ * Text RoPE fused with the append into an in-place KV cache, one launch:
+ *   q_out            = rope(q)   [B, S, Hq, D], strides (qo_sb, qo_ss, qo_sh)
+ *   k_cache[b,h,P+s] = rope(k)   cache [B, Hk, capacity, D],
+ *   v_cache[b,h,P+s] = v         strides (c_sb, c_sh, c_ss), shared by both
+ * with P = pos + (*pos_dev if pos_dev is non-NULL; a device int64, so one
+ * captured graph can append at a new position on every replay).  Rotation
+ * numerics are UMIC_ROPE_TEXT's (bf16 cos/sin, every op rounded to bf16),
+ * bit-identical to umic_rope_qk_bf16; v is moved bit for bit.  q, k, v are
+ * [B, S, H, D] with element strides (sb, ss, sh) like umic_rope_qk_bf16.
+ * Requires D % 16 == 0, every stride a multiple of 8 elements and 16-byte
+ * aligned pointers (else UMIC_ERR_UNSUPPORTED).  Without pos_dev, a write
+ * past the cache (pos < 0 or pos + S > capacity) is UMIC_ERR_INVALID_ARG
+ * and nothing is enqueued; with pos_dev, cache rows outside [0, capacity)
+ * are not written.
+ * Replaces: kernels/rope.py:86-107 (make_text_rope) followed by the cache
+ * append of cache.py:50-80 (InplaceLayer.update: slice assignment, or
+ * index_copy_ at a device position in graph mode, cache.py:53-63), as
+ * called from HF Qwen3VLTextAttention.forward (apply_rotary_pos_emb, then
+ * past_key_values.update).
+ */
+int umic_rope_kv_append_bf16(const void* q, const void* k, const void* v,
+                             void* q_out, void* k_cache, void* v_cache,
+                             const void* cos, const void* sin,
+                             int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+                             int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                             int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                             int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                             int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                             int64_t c_sb, int64_t c_sh, int64_t c_ss, int64_t capacity,
+                             int64_t pos, const int64_t* pos_dev,
+                             int64_t cs_sb, int64_t cs_ss, void* stream);
+
 /* Epilogue activations for umic_linear_bf16. */
 #define UMIC_ACT_NONE 0
 #define UMIC_ACT_GELU 1 /* exact erf GELU */

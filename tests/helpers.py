@@ -46,3 +46,27 @@ def max_rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     """max |a - b| / max |b| over the tensor."""
     a, b = a.double().cpu(), b.double().cpu()
     return float((a - b).abs().max() / b.abs().max())
+
+
+def qwen3_decoder_layer(device="cuda"):
+    """BASELINE config 5 text decoder layer (hidden 4096, 32 q / 8 kv heads,
+    head_dim 128, intermediate 12288; N(0, 0.02) weights, norms 1 + N(0, 0.1))
+    in bf16 on `device`, and its rotary embedding."""
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextDecoderLayer,
+                                                                Qwen3VLTextRotaryEmbedding)
+
+    cfg = Qwen3VLTextConfig(hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
+                            num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                            rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+                            attn_implementation="sdpa")
+    torch.manual_seed(0)
+    layer = Qwen3VLTextDecoderLayer(cfg, 0)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                p.copy_(1 + 0.1 * torch.randn_like(p))
+            else:
+                p.copy_(0.02 * torch.randn_like(p))
+    rot = Qwen3VLTextRotaryEmbedding(cfg)
+    return layer.to(torch.bfloat16).to(device).eval(), rot.to(device)

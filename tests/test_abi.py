@@ -37,7 +37,7 @@ def test_header_declares_expected_entry_points():
     for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
               "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
               "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
-              "umic_version", "umic_error_string"):
+              "umic_rope_kv_append_bf16", "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -116,6 +116,19 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_rope_qk_bf16(*args, 1, 0, 1, 4, 2, 2, 64, *strides, None) == E_UNS
     assert lib.umic_rope_qk_bf16(*args, 0, 5, 1, 4, 2, 2, 64, *strides, None) == E_ARG
     assert lib.umic_rope_qk_bf16(*args, 0, 0, 1, 0, 2, 2, 64, *strides, None) == 0
+    # rope + KV append: q, k, v, q_out, k_cache, v_cache, cos, sin; then
+    # B, S, Hq, Hk, D, 12 strides, 3 cache strides, capacity, pos, pos_dev,
+    # 2 table strides
+    kv = [fake] * 8
+    st = [8] * 12 + [8, 8, 8]
+    ok = lambda S, D, cap, pos, pos_dev=None, ptrs=kv: lib.umic_rope_kv_append_bf16(  # noqa: E731
+        *ptrs, 1, S, 4, 2, D, *st, cap, pos, pos_dev, 8, 8, None)
+    assert ok(4, 128, 16, 13) == E_ARG            # pos + S past the cache (reference raises)
+    assert ok(4, 128, 16, -1) == E_ARG            # negative position
+    assert ok(4, 120, 16, 0) == E_UNS             # D not a multiple of 16
+    assert ok(4, 128, -1, 0) == E_ARG             # negative capacity
+    assert ok(4, 128, 16, 0, ptrs=[fake] * 5 + [None] + [fake] * 2) == E_ARG  # no v cache
+    assert ok(0, 128, 16, 0, ptrs=[None] * 8) == 0   # empty: nothing launched
 
 
 def test_wrappers_refuse_cpu_tensors():

@@ -1,0 +1,176 @@
+"""CPU: the in-place KV cache (umic.cache) against transformers' DynamicCache.
+
+The in-place cache must be observably the same cache as the concatenating
+DynamicCache the reference replaces (src/umic/cache.py): the same keys and
+values after every append and crop, the same model outputs when a text model
+runs on it, an overflow error instead of a silent grow, and the graph-mode
+write at a device-held position.  On the CPU the fused-attention patch
+(``fuse_kv_rope``) takes its eager branch, so these tests also pin that branch
+(RoPE through transformers, then ``update``) against the unpatched model.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from transformers.cache_utils import DynamicCache, DynamicLayer
+
+from umic import integrate
+from umic.cache import InplaceKVCache, InplaceLayer
+
+pytestmark = pytest.mark.filterwarnings("ignore::FutureWarning")
+BF = torch.bfloat16
+
+
+def kv(B, H, S, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(B, H, S, D, generator=g).to(BF),
+            torch.randn(B, H, S, D, generator=g).to(BF))
+
+
+def text_model(layers=2):
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel
+
+    cfg = Qwen3VLTextConfig(hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                            num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                            vocab_size=64, rope_parameters={"rope_type": "default",
+                                                            "rope_theta": 1e6},
+                            attn_implementation="sdpa")
+    torch.manual_seed(0)
+    return Qwen3VLTextModel(cfg).to(BF).eval()
+
+
+def test_inplace_layer_tracks_dynamic_layer_through_appends_and_crops():
+    B, H, D, cap = 2, 3, 16, 40
+    ref = DynamicLayer()
+    k0, v0 = kv(B, H, 6, D, 0)
+    ref.update(k0, v0)
+    kb, vb = torch.zeros(B, H, cap, D, dtype=BF), torch.zeros(B, H, cap, D, dtype=BF)
+    kb[:, :, :6], vb[:, :, :6] = k0, v0
+    lyr = InplaceLayer(kb, vb, 6)
+    steps = [("add", 5), ("add", 1), ("crop", 8), ("add", 3), ("crop", -2), ("add", 1),
+             ("add", 7), ("crop", 0), ("add", 2)]
+    for i, (op, n) in enumerate(steps):
+        if op == "add":
+            k, v = kv(B, H, n, D, 10 + i)
+            rk, rv = ref.update(k, v)
+            ik, iv = lyr.update(k, v)
+            assert torch.equal(ik, rk) and torch.equal(iv, rv)
+            # single-token steps return contiguous copies, longer ones views
+            if n == 1:
+                assert ik.is_contiguous() and ik.data_ptr() != kb.data_ptr()
+            else:
+                assert ik.data_ptr() == kb.data_ptr()
+        else:
+            # crop(n): keep n tokens (n >= 0) or drop -n; DynamicLayer.crop
+            # takes the number to drop
+            keep = n if n >= 0 else ref.get_seq_length() + n
+            if keep < ref.get_seq_length():
+                ref.crop(keep - ref.get_seq_length())
+            lyr.crop(n)
+        assert lyr.get_seq_length() == ref.get_seq_length()
+        assert torch.equal(lyr.keys, ref.keys) and torch.equal(lyr.values, ref.values)
+    assert lyr.get_max_length() == cap and kb.data_ptr() == lyr._k_buf.data_ptr()
+
+
+def test_overflow_raises_and_keeps_the_cache():
+    kb, vb = torch.zeros(1, 2, 8, 4, dtype=BF), torch.zeros(1, 2, 8, 4, dtype=BF)
+    lyr = InplaceLayer(kb, vb, 6)
+    k, v = kv(1, 2, 3, 4, 1)
+    with pytest.raises(RuntimeError, match="overflow"):
+        lyr.update(k, v)
+    assert lyr.get_seq_length() == 6 and not kb[:, :, 6:].any()
+    with pytest.raises(ValueError):
+        InplaceLayer(kb, vb, 9)
+
+
+def test_from_dynamic_copies_the_prefix_once():
+    B, H, S, D = 1, 2, 5, 8
+    dyn = DynamicCache()
+    for i in range(3):
+        dyn.update(*kv(B, H, S, D, i), layer_idx=i)
+    conv = InplaceKVCache.from_dynamic(dyn, extra_tokens=10, margin=4)
+    assert len(conv.layers) == 3 and conv.get_seq_length() == S
+    for i, lyr in enumerate(conv.layers):
+        assert lyr.capacity == S + 10 + 4
+        assert torch.equal(lyr.keys, dyn.layers[i].keys)
+        assert torch.equal(lyr.values, dyn.layers[i].values)
+        assert lyr._k_buf.data_ptr() != dyn.layers[i].keys.data_ptr()
+    conv.update(*kv(B, H, 3, D, 9), layer_idx=1)
+    assert conv.get_seq_length(1) == S + 3 and conv.get_seq_length(0) == S
+    conv.crop(S)
+    assert all(lyr.get_seq_length() == S for lyr in conv.layers)
+    assert conv.get_seq_length(7) == 0
+
+
+def test_graph_mode_writes_at_the_device_position():
+    B, H, D, cap = 1, 2, 8, 12
+    dyn = DynamicCache()
+    dyn.update(*kv(B, H, 4, D, 0), layer_idx=0)
+    conv = InplaceKVCache.from_dynamic(dyn, extra_tokens=4, margin=0)
+    pos_t = torch.tensor([6])
+    conv.enable_graph_mode(pos_t)
+    conv.set_graph_len(7)
+    k, v = kv(B, H, 1, D, 3)
+    rk, rv = conv.update(k, v, 0)
+    assert rk.shape[2] == 7 and rk.is_contiguous()
+    assert torch.equal(rk[:, :, 6:7], k) and torch.equal(rv[:, :, 6:7], v)
+    assert conv.get_seq_length() == 4          # the host pointer is synced separately
+    conv.set_pos(7)
+    conv.disable_graph_mode()
+    assert conv.layers[0].keys.shape[2] == 7 and cap == 4 + 4 + 4
+    assert torch.equal(conv.layers[0].keys[:, :, 6:7], k)
+
+
+def test_text_model_on_the_inplace_cache_matches_dynamic_cache():
+    """Prefill, then an append-then-crop loop (the flow expert's pattern) on
+    both caches: hidden states and cache contents agree exactly, with the
+    fused-attention patch installed (eager branch on the CPU)."""
+    model = text_model()
+    torch.manual_seed(1)
+    pre = torch.randn(1, 20, 128).to(BF)
+    with torch.no_grad():
+        dyn = DynamicCache()
+        model(inputs_embeds=pre, past_key_values=dyn, use_cache=True)
+        conv = InplaceKVCache.from_dynamic(dyn, extra_tokens=8)
+        ref_model = text_model()
+        assert integrate.fuse_kv_rope(model) == 2
+        for step in range(3):
+            x = torch.randn(1, 8, 128).to(BF)
+            ref = ref_model(inputs_embeds=x, past_key_values=dyn, use_cache=True)
+            out = model(inputs_embeds=x, past_key_values=conv, use_cache=True)
+            assert torch.equal(out.last_hidden_state, ref.last_hidden_state), step
+            for a, b in zip(conv.layers, dyn.layers):
+                assert torch.equal(a.keys, b.keys) and torch.equal(a.values, b.values)
+            dyn.crop(-8)
+            conv.crop(20)
+    assert integrate.unfuse_mlps(model) == 2
+
+
+def test_fuse_repeat_cache_substitutes_once_and_resyncs():
+    model = text_model(layers=1)
+    seen = []
+
+    class Expert(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.lm = model
+
+        def forward(self, inputs_embeds=None, past_key_values=None):
+            seen.append(past_key_values)
+            return self.lm(inputs_embeds=inputs_embeds, past_key_values=past_key_values,
+                           use_cache=True)
+
+    expert = Expert()
+    integrate.fuse_repeat_cache(expert, extra_tokens_hint=4)
+    torch.manual_seed(2)
+    with torch.no_grad():
+        dyn = DynamicCache()
+        model(inputs_embeds=torch.randn(1, 10, 128).to(BF), past_key_values=dyn, use_cache=True)
+        for _ in range(2):
+            expert(inputs_embeds=torch.randn(1, 6, 128).to(BF), past_key_values=dyn)
+    assert isinstance(seen[0], InplaceKVCache) and seen[1] is seen[0]
+    # the caller's cache is untouched; the substitute was cropped back to it
+    assert dyn.get_seq_length() == 10 and seen[0].get_seq_length() == 16
+    assert seen[0].layers[0].capacity == 10 + 6 + 8

@@ -14,7 +14,7 @@ import collections
 
 import pytest
 import torch
-from helpers import max_rel_err, rel_err
+from helpers import max_rel_err, qwen3_decoder_layer, rel_err
 
 from umic import _lib, integrate
 
@@ -38,24 +38,7 @@ def call_log(monkeypatch):
 
 
 def decoder_layer():
-    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
-    from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextDecoderLayer,
-                                                                Qwen3VLTextRotaryEmbedding)
-
-    cfg = Qwen3VLTextConfig(hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
-                            num_attention_heads=32, num_key_value_heads=8, head_dim=128,
-                            rope_parameters={"rope_type": "default", "rope_theta": 1e6},
-                            attn_implementation="sdpa")
-    torch.manual_seed(0)
-    layer = Qwen3VLTextDecoderLayer(cfg, 0)
-    with torch.no_grad():
-        for name, p in layer.named_parameters():
-            if name.endswith("norm.weight") or "layernorm" in name:
-                p.copy_(1 + 0.1 * torch.randn_like(p))
-            else:
-                p.copy_(0.02 * torch.randn_like(p))
-    rot = Qwen3VLTextRotaryEmbedding(cfg)
-    return layer.to(torch.bfloat16).to(DEV).eval(), rot.to(DEV)
+    return qwen3_decoder_layer(DEV)
 
 
 @pytest.mark.parametrize("M", [3100, 1])

@@ -273,6 +273,107 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   }
 }
 
+// Text RoPE fused with the append into an in-place KV cache.  Per position
+// the items are q heads, then k heads, then v heads (16-byte chunk pairs as
+// above): q is rotated into q_out, k is rotated straight into the k cache and
+// v is moved bit for bit into the v cache, both at cache position P + s,
+// P = pos + (*pos_dev if given) -- a device-side P lets one captured graph
+// append at a different position on every replay.  Cache stores outside
+// [0, cap) are dropped (the host rejects them up front when P is known).
+struct KvArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* qo;
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  const int64_t* pos_dev;
+  int64_t B, S, Hq, Hk, D;
+  int64_t q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh;
+  int64_t qo_sb, qo_ss, qo_sh;
+  int64_t c_sb, c_sh, c_ss, cap, pos;
+  int64_t cs_sb, cs_ss;
+};
+
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
+  constexpr int VEC = 8;
+  const int half = (int)a.D / 2;
+  const int C = half / VEC;
+  const int nq = (int)a.Hq * C;
+  const int nk = (int)a.Hk * C;
+  const int ipp = nq + 2 * nk;
+  const int64_t nitems = a.B * a.S * ipp;
+  const int64_t P = a.pos + (a.pos_dev ? a.pos_dev[0] : 0);
+  const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const uint16_t* xs[kDirectItems];
+  uint16_t* os[kDirectItems];
+  int64_t cso[kDirectItems];
+  int dls[kDirectItems], kind[kDirectItems];  // kind: 0 q, 1 k, 2 v
+  bool ok[kDirectItems];
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    int64_t it = base + u * 256 + (int)threadIdx.x;
+    ok[u] = it < nitems;
+    if (!ok[u]) it = 0;  // re-reads item 0 (always valid) and stores nothing
+    const int64_t p = it / ipp;
+    const int j = (int)(it - p * ipp);
+    int64_t b = 0, sidx = p;
+    if (a.B != 1) {
+      b = p / a.S;
+      sidx = p - b * a.S;
+    }
+    kind[u] = j < nq ? 0 : j < nq + nk ? 1 : 2;
+    const int jj = kind[u] == 0 ? j : kind[u] == 1 ? j - nq : j - nq - nk;
+    const int h = jj / C, c = jj - h * C;
+    const int64_t t = P + sidx;  // cache position of k / v
+    if (kind[u] == 0) {
+      xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
+      os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
+    } else {
+      ok[u] = ok[u] && t >= 0 && t < a.cap;
+      const int64_t co = b * a.c_sb + h * a.c_sh + t * a.c_ss;
+      if (kind[u] == 1) {
+        xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
+        os[u] = a.kc + co;
+      } else {
+        xs[u] = a.v + b * a.v_sb + sidx * a.v_ss + h * a.v_sh;
+        os[u] = a.vc + co;
+      }
+    }
+    dls[u] = c * VEC;
+    cso[u] = b * a.cs_sb + sidx * a.cs_ss;
+  }
+  u32x4 rl[kDirectItems], rh[kDirectItems];
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    rl[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + dls[u]));
+    rh[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + half + dls[u]));
+  }
+#pragma unroll
+  for (int u = 0; u < kDirectItems; ++u) {
+    if (!ok[u]) continue;
+    u32x4* lo = reinterpret_cast<u32x4*>(os[u] + dls[u]);
+    u32x4* hi = reinterpret_cast<u32x4*>(os[u] + half + dls[u]);
+    if (kind[u] == 2) {
+      *lo = rl[u];
+      *hi = rh[u];
+      continue;
+    }
+    float xl[VEC], xh[VEC], cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
+    unpack8(rl[u], xl);
+    unpack8(rh[u], xh);
+    load_cs8<false>(a.cos, cso[u] + dls[u], cl);
+    load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
+    load_cs8<false>(a.sin, cso[u] + dls[u], sl);
+    load_cs8<false>(a.sin, cso[u] + half + dls[u], sh);
+    rotate<UMIC_ROPE_TEXT, VEC>(xl, xh, cl, ch, sl, sh, ol, oh);
+    *lo = pack8(ol);
+    *hi = pack8(oh);
+  }
+}
+
 template <int MODE, bool CS32, int VEC>
 int launch_staged(const RopeArgs& a, hipStream_t st) {
   const int64_t npos = a.B * a.S;
@@ -367,4 +468,51 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   if (mode == UMIC_ROPE_TEXT) return dispatch_vec<UMIC_ROPE_TEXT, false>(a, vec, direct_ok, st);
   if (cs_fp32) return dispatch_vec<UMIC_ROPE_VISION, true>(a, vec, direct_ok, st);
   return dispatch_vec<UMIC_ROPE_VISION, false>(a, vec, direct_ok, st);
+}
+
+extern "C" int umic_rope_kv_append_bf16(
+    const void* q, const void* k, const void* v, void* q_out, void* k_cache, void* v_cache,
+    const void* cos, const void* sin, int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+    int64_t q_sb, int64_t q_ss, int64_t q_sh, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    int64_t v_sb, int64_t v_ss, int64_t v_sh, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+    int64_t c_sb, int64_t c_sh, int64_t c_ss, int64_t capacity, int64_t pos,
+    const int64_t* pos_dev, int64_t cs_sb, int64_t cs_ss, void* stream) {
+  if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0 || capacity < 0) return UMIC_ERR_INVALID_ARG;
+  // a known write position must fit the cache (the reference raises on overflow)
+  if (!pos_dev && (pos < 0 || pos + S > capacity)) return UMIC_ERR_INVALID_ARG;
+  if (D % 16 != 0) return UMIC_ERR_UNSUPPORTED;  // 16-byte chunks of each half row
+  if ((Hq + 2 * Hk) * (D / 16) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
+  if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;
+  if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
+  if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
+  if (Hk > 0 && (!k || !v || !k_cache || !v_cache)) return UMIC_ERR_INVALID_ARG;
+
+  KvArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)q_out,
+           (uint16_t*)k_cache, (uint16_t*)v_cache, (const uint16_t*)cos, (const uint16_t*)sin,
+           pos_dev, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh,
+           qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss};
+  bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
+            (uintptr_t)sin % 16 == 0;
+  if (Hq) {
+    ok = ok && q_sb % 8 == 0 && q_ss % 8 == 0 && q_sh % 8 == 0 && qo_sb % 8 == 0 &&
+         qo_ss % 8 == 0 && qo_sh % 8 == 0 && (uintptr_t)q % 16 == 0 && (uintptr_t)q_out % 16 == 0;
+  } else {
+    a.q = a.qo = nullptr;
+  }
+  if (Hk) {
+    ok = ok && k_sb % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && v_sb % 8 == 0 &&
+         v_ss % 8 == 0 && v_sh % 8 == 0 && c_sb % 8 == 0 && c_sh % 8 == 0 && c_ss % 8 == 0 &&
+         (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && (uintptr_t)k_cache % 16 == 0 &&
+         (uintptr_t)v_cache % 16 == 0;
+  } else {
+    a.k = a.v = nullptr;
+    a.kc = a.vc = nullptr;
+  }
+  if (!ok) return UMIC_ERR_UNSUPPORTED;
+  const int64_t nitems = B * S * (Hq + 2 * Hk) * (D / 16);
+  const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     as_stream(stream), a);
+  return launch_status();
 }

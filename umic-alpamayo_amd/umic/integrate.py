@@ -483,6 +483,136 @@ def unfuse_rope() -> int:
     return n
 
 
+# ---------------------------------------------------------------------------
+# In-place KV cache: RoPE fused into the cache append
+# ---------------------------------------------------------------------------
+
+def _is_text_attention(module: nn.Module) -> bool:
+    """Structural match for the qwen3_vl text attention: q/k/v/o
+    projections, per-head q/k RMSNorms, a layer index into the cache.  The
+    class must come from the transformers qwen3_vl module, whose
+    ``apply_rotary_pos_emb`` (rotate_half convention) the kernel reproduces."""
+    mod = _qwen3_vl_module()
+    return (mod is not None and type(module).__module__ == mod.__name__
+            and all(hasattr(module, a) for a in ("q_proj", "k_proj", "v_proj", "o_proj",
+                                                 "q_norm", "k_norm", "head_dim", "layer_idx",
+                                                 "scaling", "config"))
+            and hasattr(module.config, "_attn_implementation"))
+
+
+def _attention_interface(module: nn.Module):
+    """The attention function transformers would call for `module`."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    impl = module.config._attn_implementation
+    eager = _qwen3_vl_module().eager_attention_forward
+    if impl == "eager" or impl is None:
+        return eager
+    return ALL_ATTENTION_FUNCTIONS.get_interface(impl, eager)
+
+
+def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
+                                     attention_mask=None, past_key_values=None, **kwargs):
+    """Text attention whose RoPE and KV-cache append are one kernel launch.
+
+    Taken when the cache is an ``InplaceKVCache`` and the layouts are ones
+    the kernel handles; the projections, q/k norms, attention and output
+    projection are the module's own (same order and arguments as the
+    transformers forward).  Anything else runs the class forward unchanged.
+    """
+    from umic.cache import InplaceKVCache, InplaceLayer
+
+    layer = None
+    if isinstance(past_key_values, InplaceKVCache) and self.layer_idx < len(
+            past_key_values.layers):
+        layer = past_key_values.layers[self.layer_idx]
+    if not isinstance(layer, InplaceLayer) or self.training:
+        return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
+                                  past_key_values=past_key_values, **kwargs)
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    q = self.q_norm(self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+    k = self.k_norm(self.k_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    cos, sin = position_embeddings
+    fused = layer.append_rotary(q, k, v, cos, sin)
+    if fused is not None:
+        q, k, v = fused
+    else:
+        q, k = _qwen3_vl_module().apply_rotary_pos_emb(q, k, cos, sin)
+        k, v = past_key_values.update(k, v, self.layer_idx)
+    attn = _attention_interface(self)
+    out, weights = attn(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling,
+                        **kwargs)
+    out = out.reshape(*input_shape, -1).contiguous()
+    return self.o_proj(out), weights
+
+
+def fuse_kv_rope(model: nn.Module, dry_run: bool = False) -> int:
+    """Route text attention through the fused RoPE + in-place cache append.
+
+    Only calls whose ``past_key_values`` is an ``InplaceKVCache`` change
+    path (see ``fuse_repeat_cache``); with any other cache, or none, the
+    patched forward is the class forward.
+
+    Returns:
+        Number of attention modules matched (and patched unless dry_run).
+    """
+    if _qwen3_vl_module() is None:
+        logger.warning("fuse_kv_rope: qwen3_vl module not found")
+        return 0
+    count = 0
+    for _, module in model.named_modules():
+        if not _is_text_attention(module):
+            continue
+        count += 1
+        if not dry_run:
+            module.forward = _fused_kv_rope_attention_forward.__get__(module)
+    logger.info("fuse_kv_rope: %d attention module(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
+def fuse_repeat_cache(repeat_module: nn.Module, extra_tokens_hint: int = 64) -> None:
+    """Replace per-step KV concatenation in append-then-crop loops.
+
+    Same contract as the reference (src/umic/integrate.py:715-756): a
+    forward pre-hook on `repeat_module` converts the first fully populated
+    DynamicCache it is given into an ``InplaceKVCache`` once, and on every
+    call re-syncs the substitute's write pointer to the caller's cache
+    length (an O(1) crop), so the caller's own ``crop()`` becomes redundant.
+    """
+    from transformers.cache_utils import DynamicCache
+
+    from umic.cache import InplaceKVCache
+
+    state: dict[str, object] = {"orig_id": None, "converted": None}
+
+    def _pre_hook(module, args, kwargs):
+        pkv = kwargs.get("past_key_values")
+        if pkv is None or isinstance(pkv, InplaceKVCache):
+            return None
+        if not isinstance(pkv, DynamicCache) or not getattr(pkv, "layers", None):
+            return None
+        # generate() creates the cache with lazy (keys=None) layers before
+        # prefill: convert only once every layer holds KV
+        if any(getattr(lyr, "keys", None) is None for lyr in pkv.layers):
+            return None
+        emb = kwargs.get("inputs_embeds")
+        n_new = emb.shape[1] if emb is not None else 0
+        if state["orig_id"] != id(pkv):
+            state["orig_id"] = id(pkv)
+            state["converted"] = InplaceKVCache.from_dynamic(
+                pkv, extra_tokens=max(n_new, extra_tokens_hint))
+        conv = state["converted"]
+        conv.crop(pkv.get_seq_length())
+        kwargs["past_key_values"] = conv
+        return args, kwargs
+
+    repeat_module.register_forward_pre_hook(_pre_hook, with_kwargs=True)
+    logger.info("fuse_repeat_cache: hook installed on %s", type(repeat_module).__name__)
+
+
 def unfuse_mlps(model: nn.Module) -> int:
     """Restore original forwards (delete every instance forward override)."""
     count = 0

@@ -172,5 +172,104 @@ def make_vision_rope(fallback):
     return apply_rotary_vision
 
 
+def _vec_ok(*tensors: torch.Tensor) -> bool:
+    """16-byte chunks: unit inner stride, the other strides multiples of 8
+    elements, 16-byte aligned data."""
+    for t in tensors:
+        st = t.stride()
+        if st[-1] != 1 or t.data_ptr() % 16:
+            return False
+        for s in st[:-1]:
+            if s % 8:
+                return False
+    return True
+
+
+def kv_cache_ok(k_cache: torch.Tensor, v_cache: torch.Tensor) -> bool:
+    """Cache buffers ``rope_kv_append`` writes: [B, Hk, L, D] bf16 GPU
+    tensors of one shape and stride set, D a multiple of 16, 16-byte chunks."""
+    return (isinstance(k_cache, torch.Tensor) and isinstance(v_cache, torch.Tensor)
+            and k_cache.is_cuda and k_cache.dim() == 4 and k_cache.shape == v_cache.shape
+            and k_cache.stride() == v_cache.stride() and k_cache.device == v_cache.device
+            and k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16
+            and k_cache.shape[3] % 16 == 0 and _vec_ok(k_cache, v_cache))
+
+
+def kv_inputs_ok(q, k, v, cos, sin, k_cache) -> bool:
+    """Per-call inputs ``rope_kv_append`` takes for a cache that passed
+    ``kv_cache_ok``: q [B,Hq,S,D], k and v [B,Hk,S,D] (HF's transposed
+    views or contiguous), cos/sin [B or 1, S, D], all bf16 on the cache's
+    device, 16-byte chunks."""
+    bf = torch.bfloat16
+    if not (q.dtype == bf and k.dtype == bf and v.dtype == bf and cos.dtype == bf
+            and sin.dtype == bf):
+        return False
+    dev = k_cache.device
+    if not (q.device == dev and k.device == dev and v.device == dev and cos.device == dev
+            and sin.device == dev):
+        return False
+    if q.dim() != 4 or k.dim() != 4 or cos.dim() != 3:
+        return False
+    B, _, S, D = q.shape
+    ks, cb, cs = k.shape, k_cache.shape, cos.shape
+    return (ks[0] == B and ks[2] == S and ks[3] == D and v.shape == ks
+            and cb[0] == B and cb[1] == ks[1] and cb[3] == D
+            and cs == sin.shape and cs[1] == S and cs[2] == D and cs[0] in (1, B)
+            and cos.stride() == sin.stride() and _vec_ok(q, k, v, cos, sin))
+
+
+def kv_append_eligible(q, k, v, cos, sin, k_cache, v_cache) -> bool:
+    """All of ``rope_kv_append``'s layout requirements (see the two checks)."""
+    tensors = (q, k, v, cos, sin)
+    return (all(isinstance(t, torch.Tensor) for t in tensors) and kv_cache_ok(k_cache, v_cache)
+            and kv_inputs_ok(q, k, v, cos, sin, k_cache))
+
+
+def kv_launch(q, k, v, cos, sin, k_cache, v_cache, pos: int,
+              pos_t: torch.Tensor | None) -> torch.Tensor:
+    """Launch umic_rope_kv_append_bf16 on inputs already checked by
+    ``kv_append_eligible``; returns rope(q).  The C entry point re-validates
+    strides, alignment and (without pos_t) the write range before launching."""
+    B, Hq, S, D = q.shape
+    q_out = torch.empty_like(q)
+    qs, ks, vs, os_, cst = q.stride(), k.stride(), v.stride(), q_out.stride(), k_cache.stride()
+    with _lib.device_of(q):
+        _lib.call("umic_rope_kv_append_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                  q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos.data_ptr(),
+                  sin.data_ptr(), B, S, Hq, k.shape[1], D,
+                  qs[0], qs[2], qs[1], ks[0], ks[2], ks[1], vs[0], vs[2], vs[1],
+                  os_[0], os_[2], os_[1], cst[0], cst[1], cst[2], k_cache.shape[2], pos,
+                  None if pos_t is None else pos_t.data_ptr(),
+                  cos.stride(0) if cos.shape[0] == B else 0, cos.stride(1),
+                  _lib.stream_of(q))
+    return q_out
+
+
+def rope_kv_append(q, k, v, cos, sin, k_cache, v_cache, pos: int,
+                   pos_t: torch.Tensor | None = None) -> torch.Tensor:
+    """HF text RoPE of q and k fused with the append into an in-place cache.
+
+    q [B,Hq,S,D], k/v [B,Hk,S,D] (HF's transposed views), cos/sin [B or 1,S,D]
+    bf16; k_cache/v_cache [B,Hk,L,D].  Writes rope(k) and v at cache positions
+    [P, P+S), P = pos (+ pos_t[0], an int64 device scalar, when given: the
+    replay-safe form for captured graphs), and returns rope(q) allocated like
+    eager's ``torch.empty_like(q)``.  One launch replaces the reference's
+    make_text_rope (src/umic/kernels/rope.py:86-107) plus the cache append of
+    src/umic/cache.py:59-70.  Without pos_t a write past the cache raises,
+    as the reference does (src/umic/cache.py:65-68).
+    """
+    require_device(q, k, v, cos, sin, k_cache, v_cache)
+    if not kv_append_eligible(q, k, v, cos, sin, k_cache, v_cache):
+        raise ValueError("rope_kv_append: unsupported layout "
+                         f"q{tuple(q.shape)} k{tuple(k.shape)} cache{tuple(k_cache.shape)}")
+    S, L = q.shape[2], k_cache.shape[2]
+    if pos_t is None and not (0 <= pos and pos + S <= L):
+        raise RuntimeError(f"InplaceLayer overflow: pos {pos} + new {S} > buffer {L}")
+    if pos_t is not None and not (pos_t.is_cuda and pos_t.dtype == torch.int64
+                                  and pos_t.device == q.device and pos_t.numel() >= 1):
+        raise ValueError("rope_kv_append: pos_t must be an int64 tensor on q's device")
+    return kv_launch(q, k, v, cos, sin, k_cache, v_cache, pos, pos_t)
+
+
 # Name of the reference's vision wrapper (src/umic/kernels/rope.py:78).
 apply_rotary_vision_triton = apply_rotary_vision_hip
