@@ -174,3 +174,36 @@ def test_fuse_repeat_cache_substitutes_once_and_resyncs():
     # the caller's cache is untouched; the substitute was cropped back to it
     assert dyn.get_seq_length() == 10 and seen[0].get_seq_length() == 16
     assert seen[0].layers[0].capacity == 10 + 6 + 8
+
+
+def test_decode_graph_runner_passes_cpu_calls_through():
+    """On CPU tensors the runner is a pass-through: generate() is unchanged
+    and nothing is captured."""
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLForConditionalGeneration
+
+    from umic.graph import DecodeGraphRunner
+
+    cfg = Qwen3VLConfig(
+        text_config=dict(hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                         vocab_size=256, rope_parameters={"rope_type": "default",
+                                                          "rope_theta": 1e6,
+                                                          "mrope_section": [8, 4, 4],
+                                                          "mrope_interleaved": True}),
+        vision_config=dict(depth=1, hidden_size=64, num_heads=4, intermediate_size=128,
+                           out_hidden_size=128, patch_size=4, temporal_patch_size=2,
+                           spatial_merge_size=2, num_position_embeddings=64,
+                           deepstack_visual_indexes=[]))
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    m = Qwen3VLForConditionalGeneration(cfg).to(BF).eval()
+    ids = torch.randint(0, 256, (1, 12), generator=torch.Generator().manual_seed(3))
+    kw = dict(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=4,
+              do_sample=False)
+    with torch.no_grad():
+        ref = m.generate(**kw)
+        runner = DecodeGraphRunner(m, max_new_tokens=8)
+        out = m.generate(**kw)
+    assert torch.equal(out, ref)
+    assert runner.replays == 0 and not runner.graphs and runner.cache is None

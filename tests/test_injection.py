@@ -263,13 +263,16 @@ def test_apply_report():
     assert report["ve_pipeline_fused"] == 1
     assert report["expert_rmsnorm_fused"] == 5 and report["expert_add_rmsnorm_fused"] == 1
     assert report["lm_kv_rope_fused"] == 2 and report["expert_kv_rope_fused"] == 1
-    assert report["flow_cache_hook"] is True and report["decode_cache_hook"] is True
-    assert report["decode_graph"] is False and "adaptive_flow" not in report
+    assert report["flow_cache_hook"] is True and report["decode_graph"] is True
+    assert "decode_cache_hook" not in report and "adaptive_flow" not in report
     cfg = optimize.UmicConfig(mlp_fusion=False, vision_fusion=False, decode_graph=False,
                               flow_cache=False, decode_cache=False)
     report2 = optimize.apply(_wrap(lm=tiny_text_model()), cfg)
     assert "lm_mlp_fused" not in report2 and "ve_layernorm_fused" not in report2
     assert "decode_graph" not in report2 and "decode_cache_hook" not in report2
+    report3 = optimize.apply(_wrap(lm=tiny_text_model()),
+                             optimize.UmicConfig(decode_graph=False, adaptive_flow=True))
+    assert report3["decode_cache_hook"] is True and report3["adaptive_flow"] is False
     integrate.unfuse_rope()
 
 
