@@ -234,12 +234,21 @@ def pmc_probe() -> int:
 
     _lib.load()
     torch.cuda.set_device(0)
+    from umic.kernels import rope
+
     ents, _, _ = build_workload()
     src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").normal_()
     dst = torch.empty_like(src)
     flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    # text RoPE + KV append at the prefill shape (kv_cache_step's first case)
+    S, D = 3100, 128
+    q, k, v = (_bf(1, S, H, D).transpose(1, 2) for H in (32, 8, 8))
+    kc, vc = (torch.empty(1, 8, 3200, D, dtype=torch.bfloat16, device="cuda") for _ in range(2))
+    cs = torch.randn(1, S, D, device="cuda").to(torch.bfloat16)
+    kv = ("rope_kv_append", lambda i: rope.rope_kv_append(q, k, v, cs, cs, kc, vc, 0),
+          2 * 2 * 48 * S * D + 2 * 2 * S * D)
     torch.cuda.synchronize()
-    for name, fn, nbytes, *_ in [("copy", lambda i: dst.copy_(src), 2 * COPY_BYTES)] + ents:
+    for name, fn, nbytes, *_ in [("copy", lambda i: dst.copy_(src), 2 * COPY_BYTES)] + ents + [kv]:
         flush.zero_()  # evict the Infinity Cache between probes
         torch.cuda.synchronize()
         fn(0)
