@@ -43,7 +43,14 @@ struct RopeArgs {
   int64_t q_sb, q_ss, q_sh, k_sb, k_ss, k_sh;
   int64_t qo_sb, qo_ss, qo_sh, ko_sb, ko_ss, ko_sh;
   int64_t cs_sb, cs_ss;
+  // launch-uniform divisors of the item decomposition: items per position,
+  // chunks per half row, head dim (set per launch; see SmallDiv)
+  SmallDiv ipp, chunks, dim;
 };
+
+// Items per position are bounded (checked on the host) so that every
+// in-block item offset divided by them stays below 2^22 (SmallDiv's range).
+constexpr int64_t kMaxItemsPerPos = (int64_t)1 << 21;
 
 constexpr int kMaxCsFloats = 4096;  // LDS budget per table (cos, sin): 16 KB each
 constexpr int kItems = 4;           // work items per thread per pass
@@ -118,23 +125,26 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
   const int64_t npos = a.B * a.S;
   const int D = (int)a.D;
   const int half = D / 2;
-  const int C = half / VEC;  // chunks per half row
-  const int ipp = (int)(a.Hq + a.Hk) * C;
-  const int nq = (int)a.Hq * C;
+  const int ipp = a.ipp.d;
+  const int nq = (int)a.Hq * a.chunks.d;
   // This block's flat item range [i0, i1) over (position, head, chunk) and
-  // the positions [p0, p1] it touches.
+  // the positions [p0, p1] it touches.  Block-level values in 64 bits once;
+  // per item only small offsets from (p0, r0) are divided (SmallDiv).
   const int64_t nitems = npos * ipp;
   const int64_t i0 = (int64_t)blockIdx.x * ipb;
-  const int64_t i1 = i0 + ipb < nitems ? i0 + ipb : nitems;
+  const int nloc = (int)((i0 + ipb < nitems ? i0 + ipb : nitems) - i0);
   const int64_t p0 = i0 / ipp;
-  const int np = (int)((i1 - 1) / ipp - p0 + 1);
+  const int r0 = (int)(i0 - p0 * ipp);
+  int rlast;
+  const int np = div_small(a.ipp, r0 + nloc - 1, rlast) + 1;
 
   // Stage cos/sin rows of the touched positions (fp32 in LDS; bf16 widens
   // exactly, so TEXT mode still multiplies by the bf16 values).  Run after
   // the first pass's q/k loads are in flight, so both latencies overlap.
   auto stage_tables = [&]() {
     for (int i = threadIdx.x; i < np * D; i += blockDim.x) {
-      const int pp = i / D, d = i - pp * D;
+      int d;
+      const int pp = div_small(a.dim, i, d);
       const int64_t p = p0 + pp;
       int64_t b = 0, sidx = p;
       if (a.B != 1) {
@@ -155,18 +165,19 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
   // Each thread takes kItems items per pass; all their loads are issued
   // before any is consumed (an item past the range re-reads item i0, always
   // valid, and stores nothing).
-  for (int64_t base = i0; base < i1; base += kItems * 256) {
+  for (int lbase = 0; lbase < nloc; lbase += kItems * 256) {
     const uint16_t* xs[kItems];
     uint16_t* os[kItems];
     int cofs[kItems], dls[kItems];
     bool ok[kItems];
 #pragma unroll
     for (int u = 0; u < kItems; ++u) {
-      int64_t it = base + u * 256 + (int)threadIdx.x;
-      ok[u] = it < i1;
-      if (!ok[u]) it = i0;
-      const int64_t p = it / ipp;
-      const int j = (int)(it - p * ipp);
+      int l = lbase + u * 256 + (int)threadIdx.x;
+      ok[u] = l < nloc;
+      if (!ok[u]) l = 0;
+      int j;
+      const int pp = div_small(a.ipp, r0 + l, j);
+      const int64_t p = p0 + pp;
       int64_t b = 0, sidx = p;
       if (a.B != 1) {
         b = p / a.S;
@@ -174,7 +185,8 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
       }
       const bool isq = j < nq;
       const int jj = isq ? j : j - nq;
-      const int h = jj / C, c = jj - h * C;
+      int c;
+      const int h = div_small(a.chunks, jj, c);
       if (isq) {
         xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
         os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
@@ -183,7 +195,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
         os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
       }
       dls[u] = c * VEC;
-      cofs[u] = (int)(p - p0) * D;
+      cofs[u] = pp * D;
     }
     float xl[kItems][VEC], xh[kItems][VEC];
 #pragma unroll
@@ -191,7 +203,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
       Chunk<VEC>::load(xs[u] + dls[u], xl[u]);
       Chunk<VEC>::load(xs[u] + half + dls[u], xh[u]);
     }
-    if (base == i0) {  // uniform: every thread takes the first pass
+    if (lbase == 0) {  // uniform: every thread takes the first pass
       stage_tables();
       __syncthreads();
     }
@@ -218,11 +230,13 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   const int64_t npos = a.B * a.S;
   const int D = (int)a.D;
   const int half = D / 2;
-  const int C = half / VEC;
-  const int ipp = (int)(a.Hq + a.Hk) * C;
-  const int nq = (int)a.Hq * C;
+  const int ipp = a.ipp.d;
+  const int nq = (int)a.Hq * a.chunks.d;
   const int64_t nitems = npos * ipp;
+  // block-level decomposition once, per item small divisions (SmallDiv)
   const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const int64_t pb = base / ipp;
+  const int rb = (int)(base - pb * ipp);
   const uint16_t* xs[kDirectItems];
   uint16_t* os[kDirectItems];
   int64_t cso[kDirectItems];
@@ -230,11 +244,12 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   bool ok[kDirectItems];
 #pragma unroll
   for (int u = 0; u < kDirectItems; ++u) {
-    int64_t it = base + u * 256 + (int)threadIdx.x;
-    ok[u] = it < nitems;
-    if (!ok[u]) it = 0;  // re-reads item 0 (always valid) and stores nothing
-    const int64_t p = it / ipp;
-    const int j = (int)(it - p * ipp);
+    const int l = u * 256 + (int)threadIdx.x;
+    ok[u] = base + l < nitems;
+    int j;
+    const int pp = div_small(a.ipp, rb + l, j);
+    int64_t p = pb + pp;
+    if (!ok[u]) p = 0, j = 0;  // re-reads item 0 (always valid) and stores nothing
     int64_t b = 0, sidx = p;
     if (a.B != 1) {
       b = p / a.S;
@@ -242,7 +257,8 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
     }
     const bool isq = j < nq;
     const int jj = isq ? j : j - nq;
-    const int h = jj / C, c = jj - h * C;
+    int c;
+    const int h = div_small(a.chunks, jj, c);
     if (isq) {
       xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
       os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
@@ -295,18 +311,21 @@ struct KvArgs {
   int64_t qo_sb, qo_ss, qo_sh;
   int64_t c_sb, c_sh, c_ss, cap, pos;
   int64_t cs_sb, cs_ss;
+  SmallDiv ipp, chunks;  // items per position, chunks per half row
 };
 
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
   constexpr int VEC = 8;
   const int half = (int)a.D / 2;
-  const int C = half / VEC;
-  const int nq = (int)a.Hq * C;
-  const int nk = (int)a.Hk * C;
-  const int ipp = nq + 2 * nk;
+  const int nq = (int)a.Hq * a.chunks.d;
+  const int nk = (int)a.Hk * a.chunks.d;
+  const int ipp = a.ipp.d;  // nq + 2 * nk
   const int64_t nitems = a.B * a.S * ipp;
   const int64_t P = a.pos + (a.pos_dev ? a.pos_dev[0] : 0);
+  // block-level decomposition once, per item small divisions (SmallDiv)
   const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const int64_t pb = base / ipp;
+  const int rb = (int)(base - pb * ipp);
   const uint16_t* xs[kDirectItems];
   uint16_t* os[kDirectItems];
   int64_t cso[kDirectItems];
@@ -314,11 +333,12 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
   bool ok[kDirectItems];
 #pragma unroll
   for (int u = 0; u < kDirectItems; ++u) {
-    int64_t it = base + u * 256 + (int)threadIdx.x;
-    ok[u] = it < nitems;
-    if (!ok[u]) it = 0;  // re-reads item 0 (always valid) and stores nothing
-    const int64_t p = it / ipp;
-    const int j = (int)(it - p * ipp);
+    const int l = u * 256 + (int)threadIdx.x;
+    ok[u] = base + l < nitems;
+    int j;
+    const int pp = div_small(a.ipp, rb + l, j);
+    int64_t p = pb + pp;
+    if (!ok[u]) p = 0, j = 0;  // re-reads item 0 (always valid) and stores nothing
     int64_t b = 0, sidx = p;
     if (a.B != 1) {
       b = p / a.S;
@@ -326,7 +346,8 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
     }
     kind[u] = j < nq ? 0 : j < nq + nk ? 1 : 2;
     const int jj = kind[u] == 0 ? j : kind[u] == 1 ? j - nq : j - nq - nk;
-    const int h = jj / C, c = jj - h * C;
+    int c;
+    const int h = div_small(a.chunks, jj, c);
     const int64_t t = P + sidx;  // cache position of k / v
     if (kind[u] == 0) {
       xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
@@ -374,8 +395,19 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
   }
 }
 
+// The launch-uniform divisors for vector width VEC.
+template <int VEC>
+RopeArgs with_divisors(const RopeArgs& a) {
+  RopeArgs b = a;
+  b.chunks = small_div((int)(a.D / 2 / VEC));
+  b.ipp = small_div((int)((a.Hq + a.Hk) * (a.D / 2 / VEC)));
+  b.dim = small_div((int)a.D);
+  return b;
+}
+
 template <int MODE, bool CS32, int VEC>
-int launch_staged(const RopeArgs& a, hipStream_t st) {
+int launch_staged(const RopeArgs& a0, hipStream_t st) {
+  const RopeArgs a = with_divisors<VEC>(a0);
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
   // kItems items per thread in one pass; the positions a range touches
@@ -400,7 +432,8 @@ int launch_rope(const RopeArgs& a, bool direct_ok, hipStream_t st) {
     const int64_t nitems = a.B * a.S * (a.Hq + a.Hk) * (a.D / 2 / VEC);
     const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
     if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((rope_qk_direct_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((rope_qk_direct_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       with_divisors<VEC>(a));
     return launch_status();
   } else {
     return launch_staged<MODE, CS32, VEC>(a, st);
@@ -430,7 +463,7 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
   if (mode == UMIC_ROPE_TEXT && cs_fp32) return UMIC_ERR_UNSUPPORTED;
   if (D % 2 != 0 || D > kMaxCsFloats / 4) return UMIC_ERR_UNSUPPORTED;
-  if ((Hq + Hk) * (D / 2) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
+  if ((Hq + Hk) * (D / 2) >= kMaxItemsPerPos) return UMIC_ERR_UNSUPPORTED;
   if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;  // empty: pointers may be null
   if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
   if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
@@ -481,7 +514,7 @@ extern "C" int umic_rope_kv_append_bf16(
   // a known write position must fit the cache (the reference raises on overflow)
   if (!pos_dev && (pos < 0 || pos + S > capacity)) return UMIC_ERR_INVALID_ARG;
   if (D % 16 != 0) return UMIC_ERR_UNSUPPORTED;  // 16-byte chunks of each half row
-  if ((Hq + 2 * Hk) * (D / 16) > (int64_t)1 << 30) return UMIC_ERR_UNSUPPORTED;
+  if ((Hq + 2 * Hk) * (D / 16) >= kMaxItemsPerPos) return UMIC_ERR_UNSUPPORTED;
   if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;
   if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
   if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
@@ -490,7 +523,8 @@ extern "C" int umic_rope_kv_append_bf16(
   KvArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)q_out,
            (uint16_t*)k_cache, (uint16_t*)v_cache, (const uint16_t*)cos, (const uint16_t*)sin,
            pos_dev, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh,
-           qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss};
+           qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss,
+           small_div((int)((Hq + 2 * Hk) * (D / 16))), small_div((int)(D / 16))};
   bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
             (uintptr_t)sin % 16 == 0;
   if (Hq) {
