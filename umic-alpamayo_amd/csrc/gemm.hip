@@ -141,6 +141,7 @@ struct Pipe {
   static constexpr int LB = 64 / RPI;  // direct-to-LDS loads per wave per batch
 
   int lane, grp, q, wm, wn, frow, fch, lr, opnd;
+  int nbv;  // x fragments of this wave with rows inside M (wave-uniform, 0..4)
   int arow[8], brow[4];
   // The streamed operand; its buffer resource is built inside run() (a
   // resource held in this struct loses its wave-uniformity and every load
@@ -180,6 +181,9 @@ struct Pipe {
   // group, so it fetches the chunk the swizzle places there (the swizzle of
   // tile row q*64 + j*RPI + lr depends only on lr).
   __device__ __forceinline__ void bind(const GemmArgs& g, int m0, int n0) {
+    // x rows of this wave's fragments: m0 + wm*128 + grp*64 + b*16 + [0, 16)
+    const int64_t rows_left = g.M - m0 - (wm * 128 + grp * 64);
+    nbv = rows_left <= 0 ? 0 : rows_left >= 64 ? 4 : (int)((rows_left + 15) / 16);
     const bool up = NB == 2 && grp && q >= 2;
     src = grp ? (up ? g.w1 : g.w0) : g.x;
     const int64_t ld = grp ? (up ? g.ldw1 : g.ldw0) : g.ldx;
@@ -201,21 +205,63 @@ struct Pipe {
     }
   }
 
+  // Fragments and MFMAs of the first NBV x fragments only: x rows past M
+  // would multiply range-checked zeros (the last row tile of M = 3100 has 28
+  // live rows of 256), and at the board's power limit skipped work is clock
+  // for the rest.
+  template <int NBV>
   __device__ __forceinline__ void frags(LdsRing& lds, int stage) {
+    if constexpr (NBV > 0) {
 #pragma unroll
-    for (int a = 0; a < 8; ++a)
-      fa[a] = __builtin_bit_cast(bf16x8_t, lds[stage][0][Geo::slot(arow[a] + frow, fch)]);
+      for (int a = 0; a < 8; ++a)
+        fa[a] = __builtin_bit_cast(bf16x8_t, lds[stage][0][Geo::slot(arow[a] + frow, fch)]);
+    }
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < NBV; ++b)
       fb[b] = __builtin_bit_cast(bf16x8_t, lds[stage][1][Geo::slot(brow[b] + frow, fch)]);
   }
 
+  template <int NBV>
   __device__ __forceinline__ void compute() {
 #pragma unroll
     for (int a = 0; a < 8; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < NBV; ++b)
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+  }
+
+  // The K loop of one group for NBV live x fragments (see run()).  Every
+  // NBV passes the same barriers: the phases differ only in the MFMAs and
+  // fragment reads they contain.
+  template <int NBV>
+  __device__ __forceinline__ void loop(LdsRing& lds, __amdgpu_buffer_rsrc_t rs, int k0, int n) {
+    if (grp == 0) frags<NBV>(lds, 0);
+    stage_barrier<(D - 1) * LB>();
+    if (grp == 0) {
+      for (int j = 0; j < n; ++j) {
+        compute<NBV>();
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 2) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+        frags<NBV>(lds, (j + 1) % S);
+        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      for (int j = 0; j < n; ++j) {
+        frags<NBV>(lds, j % S);
+        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+        compute<NBV>();
+        __builtin_amdgcn_sched_barrier(0);
+        stage_barrier<(D - 1) * LB>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
 
   // acc = the tile's products over K steps [k0, k1) (k1 > k0).  Prologue: D
@@ -227,6 +273,7 @@ struct Pipe {
   // the last steps' refills land asynchronously, and each wave's
   // s_waitcnt covers only its own, so a barrier follows before anyone
   // writes the ring (staged output, the arrival word, the next prologue).
+  template <bool SKIP_DEAD_ROWS = true>
   __device__ __forceinline__ void run(LdsRing& lds, int k0, int k1) {
 #pragma unroll
     for (int a = 0; a < 8; ++a)
@@ -240,36 +287,23 @@ struct Pipe {
 #pragma unroll
     for (int s = 0; s < D; ++s) issue(lds, rs, s, (k0 + s) * kBK);
     stage_barrier<(D - 1) * LB>();
-    if (grp == 0) frags(lds, 0);
-    stage_barrier<(D - 1) * LB>();
     // One straight loop per group (the hardware barrier counts arrivals,
     // not program points; both loops pass the same barriers), so the
     // fragments stay loop-carried in place.  sched_barrier keeps every MFMA
-    // in its phase.
-    if (grp == 0) {
-      for (int j = 0; j < n; ++j) {
-        compute();
-        __builtin_amdgcn_sched_barrier(0);
-        stage_barrier<(D - 2) * LB>();
-        __builtin_amdgcn_sched_barrier(0);
-        frags(lds, (j + 1) % S);
-        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_barrier<(D - 1) * LB>();
-        __builtin_amdgcn_sched_barrier(0);
+    // in its phase.  The loop is instantiated per count of live x fragments
+    // (wave-uniform, fixed for the tile): 4 everywhere but the last row tile.
+    // (The stream-K kernel keeps one full loop: the extra instantiations'
+    // register state would spill there.)
+    if constexpr (SKIP_DEAD_ROWS) {
+      switch (nbv) {
+        case 4: loop<4>(lds, rs, k0, n); break;
+        case 3: loop<3>(lds, rs, k0, n); break;
+        case 2: loop<2>(lds, rs, k0, n); break;
+        case 1: loop<1>(lds, rs, k0, n); break;
+        default: loop<0>(lds, rs, k0, n); break;
       }
     } else {
-      for (int j = 0; j < n; ++j) {
-        frags(lds, j % S);
-        issue(lds, rs, (j + D) % S, (k0 + j + D) * kBK);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_barrier<(D - 1) * LB>();
-        __builtin_amdgcn_sched_barrier(0);
-        compute();
-        __builtin_amdgcn_sched_barrier(0);
-        stage_barrier<(D - 1) * LB>();
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      loop<4>(lds, rs, k0, n);
     }
     stage_barrier<0>();
   }
@@ -503,7 +537,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
     asm volatile("" : "+v"(vt));
     p.init(vt);
     p.bind(g, m0, n0);
-    p.run(lds, k0, k1);
+    p.template run<false>(lds, k0, k1);
     const int nseg = s.ks == s.KT ? 1
                                   : 2 + tl.owner(t * tl.L + tl.L - 1) - tl.owner(t * tl.L);
     if (nseg == 1) {
