@@ -207,3 +207,35 @@ def test_decode_graph_runner_passes_cpu_calls_through():
         out = m.generate(**kw)
     assert torch.equal(out, ref)
     assert runner.replays == 0 and not runner.graphs and runner.cache is None
+
+
+def test_flow_step_graph_falls_back_to_eager_on_cpu():
+    """FlowStepGraph on CPU tensors: capture is unavailable, so after the
+    warm-up steps it falls back to eager for good, with the same results;
+    fuse_flow_graph wraps the step closures handed to diffusion.sample."""
+    from umic.graph import FlowStepGraph, fuse_flow_graph
+
+    calls = []
+
+    def step_fn(x, t):
+        calls.append(1)
+        return x * 2 + t
+
+    fsg = FlowStepGraph(step_fn, warmup=2)
+    xs = [torch.randn(1, 4, 8) for _ in range(5)]
+    for i, x in enumerate(xs):
+        t = torch.full((1,), float(i))
+        assert torch.equal(fsg(x, t), x * 2 + t)
+    assert fsg.failed and fsg.graph is None and len(calls) == 5
+
+    class Diffusion:
+        def sample(self, noise, step_fn=None, unguided_step_fn=None):
+            self.seen = (step_fn, unguided_step_fn)
+            return step_fn(x=noise, t=torch.zeros(1))
+
+    model = torch.nn.Module()
+    model.diffusion = Diffusion()
+    fuse_flow_graph(model)
+    x = torch.randn(2, 3)
+    assert torch.equal(model.diffusion.sample(x, step_fn=step_fn), x * 2)
+    assert isinstance(model.diffusion.seen[0], FlowStepGraph) and model.diffusion.seen[1] is None

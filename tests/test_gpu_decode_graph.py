@@ -1,5 +1,7 @@
-"""GPU: decode-step HIP graphs (umic.graph.DecodeGraphRunner) on a small
-random-weight Qwen3-VL, text-only prompts, greedy generate().
+"""GPU: decode-step and flow-step HIP graphs (umic.graph).
+
+DecodeGraphRunner, on a small random-weight Qwen3-VL, text-only prompts,
+greedy generate():
 
 The same prompts are decoded eagerly by the unpatched model first; then the
 LM gets the fused kernels (RMSNorm, add+RMSNorm, text RoPE, RoPE + in-place
@@ -101,3 +103,49 @@ def test_decode_graph_runner_matches_eager(monkeypatch):
     assert captured == [NEW - 3, NEW - 1, NEW - 1, NEW - 3]
     assert runner.replays == (NEW - 3) + (NEW - 1) + (NEW - 1) + (NEW - 3)
     assert log["umic_rope_kv_append_bf16"] > 0      # the fused append ran in the graphs
+
+
+def test_flow_step_graph_replays_match_eager():
+    """FlowStepGraph over a flow-expert-like step: 32 action tokens through a
+    config-5 decoder layer that appends to an in-place KV cache (RoPE and the
+    append fused) and attends to the whole prefix, then crops back.  Ten
+    steps with new x and t: each replay equals the eager step bit for bit,
+    and the cache prefix is untouched."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from transformers.cache_utils import DynamicCache
+
+    from helpers import qwen3_decoder_layer
+    from umic.cache import InplaceKVCache
+    from umic.graph import FlowStepGraph
+
+    layer, rot = qwen3_decoder_layer(DEV)
+    P, N = 1024, 32
+    torch.manual_seed(11)
+    h0 = torch.randn(1, P, 4096).to(torch.bfloat16).to(DEV)
+    with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION,
+                                       SDPBackend.EFFICIENT_ATTENTION]):
+        dyn = DynamicCache()
+        layer(h0, position_embeddings=rot(h0, torch.arange(P, device=DEV)[None]),
+              past_key_values=dyn)
+        cache = InplaceKVCache.from_dynamic(dyn, extra_tokens=N)
+        prefix_k = cache.layers[0].keys.clone()
+        assert integrate.fuse_kv_rope(layer) == 1
+        cs = rot(h0[:, :N], torch.arange(P, P + N, device=DEV)[None])
+
+        def step_fn(x, t):
+            out = layer(x + t, position_embeddings=cs, past_key_values=cache, is_causal=False)
+            cache.crop(P)
+            return out
+
+        fsg = FlowStepGraph(step_fn, warmup=2)
+        g = torch.Generator().manual_seed(12)
+        for i in range(10):
+            x = torch.randn(1, N, 4096, generator=g).to(torch.bfloat16).to(DEV)
+            t = torch.full((1, 1, 1), 0.1 * i).to(torch.bfloat16).to(DEV)
+            ref = step_fn(x=x, t=t)
+            out = fsg(x, t)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), i
+        assert fsg.graph is not None and not fsg.failed
+        assert torch.equal(cache.layers[0]._k_buf[:, :, :P], prefix_k)
+    integrate.unfuse_mlps(layer)

@@ -1,4 +1,8 @@
-"""Decode-step HIP graphs: one captured graph per KV length, replayed.
+"""Decode-step and flow-step HIP graphs.
+
+``DecodeGraphRunner``: one captured graph per KV length, replayed.
+``FlowStepGraph`` / ``fuse_flow_graph``: one graph for the fixed-shape flow
+ODE step (see their docstrings).
 
 Same contract as the reference's decode runner (src/umic/graph.py:36-176):
 the runner wraps the VLM's ``forward`` (instance attribute, so module hooks
@@ -226,3 +230,73 @@ def fuse_decode_graph(vlm: torch.nn.Module, max_new_tokens: int = 96) -> DecodeG
     """Install the per-length decode graph runner on the VLM
     (src/umic/graph.py:179-181)."""
     return DecodeGraphRunner(vlm, max_new_tokens=max_new_tokens)
+
+
+class FlowStepGraph:
+    """One captured graph for a fixed-shape flow ODE step, replayed per step.
+
+    Same contract as src/umic/graph.py:179-232.  Every step of the flow
+    expert runs ``step_fn(x=, t=)`` on the same shapes: its action tokens are
+    appended to the prefix KV at the same cache rows and cropped back, so the
+    buffers the kernels touch are identical each step and only the values of
+    x and t change.  After ``warmup`` eager steps the step is captured once
+    (on static copies of x and t); later steps copy x and t in and replay.
+    With ``umic.integrate.fuse_kv_rope`` the attention's RoPE and cache write
+    inside the graph is one launch at the baked cache position.  A capture
+    that fails falls back to eager for good, so results never depend on it.
+    The graph holds the buffer addresses of the cache it was captured on:
+    build a new one per inference (per prompt cache).
+    """
+
+    def __init__(self, step_fn, warmup: int = 2) -> None:
+        self.step_fn = step_fn
+        self.warmup = warmup
+        self.n = 0
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.xs: torch.Tensor | None = None
+        self.ts: torch.Tensor | None = None
+        self.out: torch.Tensor | None = None
+        self.failed = False
+
+    def __call__(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+        if self.failed or (self.graph is None and self.n < self.warmup):
+            self.n += 1
+            return self.step_fn(x=x, t=t)
+        if self.graph is None:
+            try:
+                self.xs, self.ts = x.clone(), t.clone()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    self.step_fn(x=self.xs, t=self.ts)
+                torch.cuda.current_stream().wait_stream(side)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    self.out = self.step_fn(x=self.xs, t=self.ts)
+                self.graph = graph
+                logger.info("FlowStepGraph captured (step %d)", self.n)
+            except Exception as exc:  # noqa: BLE001 -- correctness first
+                logger.warning("FlowStepGraph: capture failed (%s); eager steps", exc)
+                self.failed = True
+                return self.step_fn(x=x, t=t)
+        self.n += 1
+        self.xs.copy_(x)
+        self.ts.copy_(t)
+        self.graph.replay()
+        return self.out.clone()
+
+
+def fuse_flow_graph(model: torch.nn.Module, warmup: int = 2) -> None:
+    """Wrap the step closures ``model.diffusion.sample`` receives in
+    ``FlowStepGraph`` (src/umic/graph.py:235-253); nothing else changes."""
+    diffusion = model.diffusion
+    orig_sample = diffusion.sample
+
+    def sample(*args, **kwargs):
+        for key in ("step_fn", "unguided_step_fn"):
+            if kwargs.get(key) is not None:
+                kwargs[key] = FlowStepGraph(kwargs[key], warmup)
+        return orig_sample(*args, **kwargs)
+
+    diffusion.sample = sample
+    logger.info("fuse_flow_graph: flow ODE step graph runner installed")
