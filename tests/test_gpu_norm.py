@@ -23,11 +23,14 @@ DEV = "cuda"
 
 # (rows, n): BASELINE shapes, decode row, empty, q/k_norm rows, ragged lane
 # tails (n=1000, 80), rows beyond the register path (n=8200, 16384) and
-# n % 8 != 0 (generic kernel).
+# n % 8 != 0 (generic kernel).  Rows of one or two vectors per lane take 4 or
+# 2 rows per lane group from 16384 rows up: (99200, 128) and (24800, 128) do,
+# (16390, 128) and (16387, 1024) with a ragged last group, (64, 128) does not.
 RMS_SHAPES = [(3100, 4096), (257, 4096), (1, 4096), (0, 4096), (99200, 128), (24800, 128),
+              (16390, 128), (16387, 1024), (64, 128),
               (333, 1280), (64, 1000), (77, 80), (9, 8200), (5, 16384), (31, 100), (3, 2)]
 LN_SHAPES = [(16384, 1280), (4096, 1152), (100, 4096), (1, 1280), (0, 1280), (64, 1000),
-             (50, 80), (7, 8200), (13, 100)]
+             (16390, 128), (16387, 1024), (50, 80), (7, 8200), (13, 100)]
 
 
 def _inputs(rows, n, seed):

@@ -43,108 +43,138 @@ struct NormArgs {
 
 // ---- register-resident fast path -----------------------------------------
 
-template <int OP, int LPR, int MAXV>
+// RPG rows per group: rows of one or two vectors per lane (e.g. the
+// [S*H, 128] per-head q/k norms) leave a wavefront only 1-2 KB of loads in
+// flight, too little to cover HBM latency; a group then takes RPG
+// consecutive rows and issues all their loads before reducing any.
+template <int OP, int LPR, int MAXV, int RPG>
 __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, int vpl) {
-  const int rows_per_block = (int)blockDim.x / LPR;
+  const int rows_per_block = (int)blockDim.x / LPR * RPG;
   const int lane = threadIdx.x & (LPR - 1);
-  const int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / LPR;
-  // All LPR lanes of a group share `row`, so a group exits as a whole and
+  const int64_t row0 = (int64_t)blockIdx.x * rows_per_block + (threadIdx.x / LPR) * RPG;
+  // All LPR lanes of a group share its rows, so a group exits as a whole and
   // the butterflies below only ever read lanes of a live group.
-  if (row >= a.rows) return;
+  if (row0 >= a.rows) return;
 
-  // The row's source values stay packed as bf16 (16 B per 8 elements) in
+  // The rows' source values stay packed as bf16 (16 B per 8 elements) in
   // registers between the statistics pass and the output pass.  Loads are
-  // issued unconditionally (a dead slot re-reads vector 0 and is zeroed by a
-  // select): predicated loads would sit in branches, and every branch join
-  // costs a full vmcnt drain -- the loads must all be in flight together.
-  const u32x4* xp = reinterpret_cast<const u32x4*>(a.x + row * a.ldx);
+  // issued unconditionally (a dead slot re-reads vector 0, a row past the
+  // end re-reads row0; both are zeroed or never stored): predicated loads
+  // would sit in branches, and every branch join costs a full vmcnt drain
+  // -- the loads must all be in flight together.
   const u32x4 zero = {0u, 0u, 0u, 0u};
   bool live[MAXV];
   int cix[MAXV];
-  u32x4 sv[MAXV];
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int c = i * LPR + lane;
     live[i] = i < vpl && c < nvec;
     cix[i] = live[i] ? c : 0;
-    sv[i] = ld_stream(xp + cix[i]);
+  }
+  bool rlive[RPG];
+  int64_t rows[RPG];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    rlive[r] = r == 0 || row0 + r < a.rows;  // row0 is live (checked above)
+    rows[r] = rlive[r] ? row0 + r : row0;
+  }
+  u32x4 sv[RPG][MAXV];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    const u32x4* xp = reinterpret_cast<const u32x4*>(a.x + rows[r] * a.ldx);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) sv[r][i] = ld_stream(xp + cix[i]);
   }
   if constexpr (has_add(OP)) {
-    const u32x4* rp = reinterpret_cast<const u32x4*>(a.r + row * a.ldr);
-    u32x4 rv[MAXV];
+    u32x4 rv[RPG][MAXV];
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i) rv[i] = ld_stream(rp + cix[i]);
+    for (int r = 0; r < RPG; ++r) {
+      const u32x4* rp = reinterpret_cast<const u32x4*>(a.r + rows[r] * a.ldr);
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i) {
-      float xf[8], rf[8];
-      unpack8(sv[i], xf);
-      unpack8(rv[i], rf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xf[e] = xf[e] + rf[e];
-      sv[i] = pack8(xf);  // bf16(x + r): the eager residual add
+      for (int i = 0; i < MAXV; ++i) rv[r][i] = ld_stream(rp + cix[i]);
     }
-    u32x4* sp = reinterpret_cast<u32x4*>(a.s + row * a.lds);
 #pragma unroll
-    for (int i = 0; i < MAXV; ++i)
-      if (live[i]) st_stream(sp + cix[i], sv[i]);
-  }
+    for (int r = 0; r < RPG; ++r) {
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) sv[i] = live[i] ? sv[i] : zero;
-
-  // Exact double sums (zero-filled tail vectors contribute nothing).  Four
-  // independent accumulators keep the f64 add chains short; the sums are
-  // exact, so the grouping does not change them.
-  double sum4[4] = {0.0, 0.0, 0.0, 0.0}, ssq4[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int i = 0; i < MAXV; ++i) {
+        float xf[8], rf[8];
+        unpack8(sv[r][i], xf);
+        unpack8(rv[r][i], rf);
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    float f[8];
-    unpack8(sv[i], f);
+        for (int e = 0; e < 8; ++e) xf[e] = xf[e] + rf[e];
+        sv[r][i] = pack8(xf);  // bf16(x + r): the eager residual add
+      }
+      u32x4* sp = reinterpret_cast<u32x4*>(a.s + rows[r] * a.lds);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if constexpr (is_ln(OP)) sum4[e & 3] += (double)f[e];
-      ssq4[e & 3] += (double)(f[e] * f[e]);  // a bf16 square is exact in fp32
+      for (int i = 0; i < MAXV; ++i)
+        if (live[i] && rlive[r]) st_stream(sp + cix[i], sv[r][i]);
     }
-  }
-  double sum = (sum4[0] + sum4[1]) + (sum4[2] + sum4[3]);
-  double ssq = (ssq4[0] + ssq4[1]) + (ssq4[2] + ssq4[3]);
-  const double inv_n = 1.0 / (double)a.n;
-  float rstd, mean = 0.f;
-  if constexpr (is_ln(OP)) {
-    sum = group_sum<LPR>(sum);
-    ssq = group_sum<LPR>(ssq);
-    const double mean_d = sum * inv_n;
-    mean = (float)mean_d;
-    rstd = rsqrt_cr((float)(ssq * inv_n - mean_d * mean_d) + a.eps);
-  } else {
-    rstd = rsqrt_cr((float)(group_sum<LPR>(ssq) * inv_n) + a.eps);
   }
 
   const u32x4* wp = reinterpret_cast<const u32x4*>(a.w);
   const u32x4* bp = reinterpret_cast<const u32x4*>(a.b);
-  u32x4* yp = reinterpret_cast<u32x4*>(a.y + row * a.ldy);
   u32x4 wv[MAXV], bv[MAXV];
+  const double inv_n = 1.0 / (double)a.n;
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    wv[i] = wp[cix[i]];
-    if constexpr (is_ln(OP)) bv[i] = bp[cix[i]];
-  }
+  for (int r = 0; r < RPG; ++r) {
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    if (!live[i]) continue;
-    const int c = cix[i];
-    float f[8], wf[8], o[8];
-    unpack8(sv[i], f);
-    unpack8(wv[i], wf);
-    if constexpr (is_ln(OP)) {
-      float bf[8];
-      unpack8(bv[i], bf);
+    for (int i = 0; i < MAXV; ++i) sv[r][i] = live[i] ? sv[r][i] : zero;
+
+    // Exact double sums (zero-filled tail vectors contribute nothing).  Four
+    // independent accumulators keep the f64 add chains short; the sums are
+    // exact, so the grouping does not change them.
+    double sum4[4] = {0.0, 0.0, 0.0, 0.0}, ssq4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wf[e], rstd * (f[e] - mean), bf[e]);
-    } else {
+    for (int i = 0; i < MAXV; ++i) {
+      float f[8];
+      unpack8(sv[r][i], f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (is_ln(OP)) sum4[e & 3] += (double)f[e];
+        ssq4[e & 3] += (double)(f[e] * f[e]);  // a bf16 square is exact in fp32
+      }
     }
-    st_stream(yp + c, pack8(o));
+    double sum = (sum4[0] + sum4[1]) + (sum4[2] + sum4[3]);
+    double ssq = (ssq4[0] + ssq4[1]) + (ssq4[2] + ssq4[3]);
+    float rstd, mean = 0.f;
+    if constexpr (is_ln(OP)) {
+      sum = group_sum<LPR>(sum);
+      ssq = group_sum<LPR>(ssq);
+      const double mean_d = sum * inv_n;
+      mean = (float)mean_d;
+      rstd = rsqrt_cr((float)(ssq * inv_n - mean_d * mean_d) + a.eps);
+    } else {
+      rstd = rsqrt_cr((float)(group_sum<LPR>(ssq) * inv_n) + a.eps);
+    }
+    if (r == 0) {
+      // weights (and bias), L2-resident, loaded once the first row's
+      // statistics are done: issued with the row loads they measured slower
+#pragma unroll
+      for (int i = 0; i < MAXV; ++i) {
+        wv[i] = wp[cix[i]];
+        if constexpr (is_ln(OP)) bv[i] = bp[cix[i]];
+      }
+    }
+
+    u32x4* yp = reinterpret_cast<u32x4*>(a.y + rows[r] * a.ldy);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      if (!live[i] || !rlive[r]) continue;
+      const int c = cix[i];
+      float f[8], wf[8], o[8];
+      unpack8(sv[r][i], f);
+      unpack8(wv[i], wf);
+      if constexpr (is_ln(OP)) {
+        float bf[8];
+        unpack8(bv[i], bf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wf[e], rstd * (f[e] - mean), bf[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+      }
+      st_stream(yp + c, pack8(o));
+    }
   }
 }
 
@@ -211,23 +241,37 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(NormArgs a) {
 // Block size: the hardware spreads workgroups evenly over the 256 CUs only
 // when there are many of them, so small row counts get 64- or 128-thread
 // blocks (the largest block that still yields >= 8 blocks per CU).
-template <int OP, int LPR, int MAXV>
+template <int OP, int LPR, int MAXV, int RPG = 1>
 int launch_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
   int threads = 256;
-  while (threads > 64 && (a.rows * LPR + threads - 1) / threads < 8 * 256) threads >>= 1;
-  const int rows_per_block = threads / LPR;
+  while (threads > 64 && (a.rows * LPR / RPG + threads - 1) / threads < 8 * 256) threads >>= 1;
+  const int rows_per_block = threads / LPR * RPG;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((norm_rows_kernel<OP, LPR, MAXV>), dim3((unsigned)blocks), dim3(threads), 0,
-                     st, a, nvec, vpl);
+  hipLaunchKernelGGL((norm_rows_kernel<OP, LPR, MAXV, RPG>), dim3((unsigned)blocks), dim3(threads),
+                     0, st, a, nvec, vpl);
   return launch_status();
+}
+
+// One- and two-vector rows take 4 or 2 rows per group when the grouped
+// launch still has >= 16 wavefronts per CU (measured on the [S*H, 128]
+// per-head norms: 99200 rows gain ~10%, 24800 rows lose ~18% with grouping);
+// smaller launches keep one row per group, spread over more wavefronts.
+constexpr int64_t kRpgMinThreads = (int64_t)256 * 16 * 64;
+
+template <int OP, int LPR, int MAXV>
+int launch_small_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
+  constexpr int kRpg = MAXV == 1 ? 4 : 2;
+  if (a.rows * LPR / kRpg >= kRpgMinThreads)
+    return launch_rows<OP, LPR, MAXV, kRpg>(a, nvec, vpl, st);
+  return launch_rows<OP, LPR, MAXV>(a, nvec, vpl, st);
 }
 
 template <int OP, int LPR>
 int launch_lpr(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
   switch (vpl) {
-    case 1: return launch_rows<OP, LPR, 1>(a, nvec, vpl, st);
-    case 2: return launch_rows<OP, LPR, 2>(a, nvec, vpl, st);
+    case 1: return launch_small_rows<OP, LPR, 1>(a, nvec, vpl, st);
+    case 2: return launch_small_rows<OP, LPR, 2>(a, nvec, vpl, st);
     case 3: return launch_rows<OP, LPR, 3>(a, nvec, vpl, st);
     case 4: return launch_rows<OP, LPR, 4>(a, nvec, vpl, st);
     case 5: return launch_rows<OP, LPR, 5>(a, nvec, vpl, st);
