@@ -490,13 +490,15 @@ def vit_sites() -> int:
         return e0.elapsed_time(e1) / reps * 1e3
 
     M = 16384
+    approx = {"gelu": "none", "gelu_tanh": "tanh"}
     for site, K, N, act in (("qkv", 1280, 3840, None), ("fc1_gelu", 1280, 5120, "gelu"),
+                            ("fc1_gelu_tanh", 1280, 5120, "gelu_tanh"),
                             ("fc2", 5120, 1280, None)):
         x = _bf(M, K)
         w, b = _bf(N, K, scale=0.02), _bf(N, scale=0.1)
         ours = timed(lambda: linear.linear_hip(x, w, b, act=act))
         if act:
-            vendor = timed(lambda: F.gelu(F.linear(x, w, b)))
+            vendor = timed(lambda: F.gelu(F.linear(x, w, b), approximate=approx[act]))
         else:
             vendor = timed(lambda: F.linear(x, w, b))
         print(json.dumps({"site": site, "M": M, "K": K, "N": N, "act": act,

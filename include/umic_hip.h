@@ -151,7 +151,8 @@ int umic_rope_kv_append_bf16(const void* q, const void* k, const void* v,
 
 /* Epilogue activations for umic_linear_bf16. */
 #define UMIC_ACT_NONE 0
-#define UMIC_ACT_GELU 1 /* exact erf GELU */
+#define UMIC_ACT_GELU 1      /* exact erf GELU */
+#define UMIC_ACT_GELU_TANH 2 /* tanh-approximate GELU (torch approximate="tanh") */
 
 /*
  * out = act(x @ w^T + bias), bf16 in/out, fp32 accumulation on MFMA.

@@ -165,7 +165,7 @@ def gate_silu_mul(x, wg, wu, fused: bool = True) -> np.ndarray:
 
 
 def linear(x, w, bias=None, act: int = 0, fused: bool = True) -> np.ndarray:
-    """act(x @ w^T + bias); w: [N, K] bf16 bits; act 0 none / 1 erf-GELU."""
+    """act(x @ w^T + bias); w: [N, K] bf16 bits; act 0 none / 1 erf-GELU / 2 tanh-GELU."""
     x, w = _u16(x), _u16(w)
     b = None if bias is None else _u16(bias)
     (M, K), (N, K2) = x.shape, w.shape

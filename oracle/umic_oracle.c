@@ -220,6 +220,13 @@ static inline float silu_f(float g) { return g / (1.0f + expf(-g)); }
 static inline float gelu_erf_f(float v) {
   return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
 }
+/* torch's gelu(approximate="tanh") in fp32 (HF gelu_pytorch_tanh), with its
+ * operation order: inner = sqrt(2/pi) * (v + 0.044715 * v^3). */
+static inline float gelu_tanh_f(float v) {
+  const float cube = v * v * v;
+  const float inner = 0.7978845608028654f * (v + 0.044715f * cube);
+  return 0.5f * v * (1.0f + tanhf(inner));
+}
 
 /* P5: silu(x @ wg^T) * (x @ wu^T).
  * fused = 1: the reference kernel's numerics, kernels/fused_ffn.py:71-91
@@ -253,7 +260,9 @@ void orc_gate_silu_mul(const uint16_t* x, const uint16_t* wg, const uint16_t* wu
 /* Linear with optional bias and erf-GELU epilogue, reference kernel
  * kernels/linear.py:32-90 (acc + bias, GELU, one rounding).
  * fused = 0 restates the eager pair F.linear -> bf16, then GELU -> bf16.
- * bias may be NULL.  act: 0 none, 1 erf GELU. */
+ * bias may be NULL.  act: 0 none, 1 erf GELU, 2 tanh-approximate GELU (the
+ * activation of the Qwen3-VL ViT MLP; the reference's epilogue has no such
+ * mode, kernels/linear.py:83-86 always applies the erf form). */
 void orc_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                 uint16_t* out, int64_t M, int64_t N, int64_t K, int act,
                 int fused) {
@@ -267,6 +276,7 @@ void orc_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
       if (bias) v = v + bf2f(bias[n]);
       if (!fused) v = rbf(v);
       if (act == 1) v = gelu_erf_f(v);
+      if (act == 2) v = gelu_tanh_f(v);
       out[m * N + n] = f2bf(v);
     }
 }

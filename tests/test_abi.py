@@ -95,6 +95,7 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 80, 80, 80, 64, 0, None) == E_UNS
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 60, 128, 128, 128, 60, 0, None) == E_UNS
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 7, None) == E_ARG
+    assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 3, None) == E_ARG
     assert lib.umic_linear_bf16(fake, fake, None, fake, 0, 64, 128, 128, 128, 64, 0, None) == 0
     assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
                                        None) == E_ARG

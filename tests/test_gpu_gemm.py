@@ -48,10 +48,10 @@ def test_linear_bias_gelu_vs_oracle():
     M, N, K = 200, 392, 192
     x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.1, gen=g)
     b = bf16_randn(N, scale=0.5, gen=g)
-    for act in (None, "gelu"):
+    for act, code in ((None, 0), ("gelu", 1), ("gelu_tanh", 2)):
         y = linear.linear_hip(x.to(DEV), w.to(DEV), b.to(DEV), act=act)
         torch.cuda.synchronize()
-        _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), 1 if act else 0, fused=True))
+        _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), code, fused=True))
 
 
 def test_linear_strided_x_and_leading_dims():
@@ -112,15 +112,16 @@ def test_linear_stream_k_vs_oracle(M, N, K, calls):
         _check_vs_oracle(y, oracle.linear(bits(x), bits(w), None, 0, fused=True))
 
 
-def test_linear_stream_k_bias_gelu_vs_oracle():
+@pytest.mark.parametrize("act,code", [("gelu", 1), ("gelu_tanh", 2)])
+def test_linear_stream_k_bias_gelu_vs_oracle(act, code):
     M, N, K = 300, 264, 12288
     assert _sk_bytes(M, N, K) > 0
     g = torch.Generator().manual_seed(11)
     x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.02, gen=g)
     b = bf16_randn(N, scale=0.5, gen=g)
-    y = linear.linear_hip(x.to(DEV), w.to(DEV), b.to(DEV), act="gelu")
+    y = linear.linear_hip(x.to(DEV), w.to(DEV), b.to(DEV), act=act)
     torch.cuda.synchronize()
-    _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), 1, fused=True))
+    _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), code, fused=True))
 
 
 def test_stream_k_deterministic_and_close_to_data_parallel():

@@ -95,6 +95,7 @@ def test_vision_pipeline_on_gpu(call_log):
         integrate.fuse_layernorms(m)
         assert integrate.fuse_vision_rope()
         assert integrate.fuse_vision_encoder_pipeline(m) == 1
+        assert integrate.fuse_gelu_mlps(m) == 4
         out = m(px, grid_thw=grid)
         torch.cuda.synchronize()
     for a, b in ((out.last_hidden_state, ref.last_hidden_state),
@@ -107,3 +108,36 @@ def test_vision_pipeline_on_gpu(call_log):
     assert call_log["umic_rope_qk_bf16"] == 4
     assert call_log["umic_add_layernorm_bf16"] == 4 + 2 + 1
     assert call_log["umic_layernorm_bf16"] == 2 + 1   # block 0 and 2 norm1, deepstack merger
+    assert call_log["umic_linear_ws_bf16"] == 4       # each block's fc1 + tanh GELU
+
+
+@pytest.mark.parametrize("act,rows", [("gelu_pytorch_tanh", 16384), ("gelu", 4100),
+                                      ("gelu_pytorch_tanh", 63)])
+def test_vit_gelu_mlp_module(act, rows, call_log):
+    """The ViT MLP block at BASELINE's ViT width (hidden 1280, 4x MLP): fused
+    fc1 + GELU then the vendor fc2, against the unpatched module; 63 rows stay
+    on the eager path and match it bit for bit."""
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionMLP
+
+    cfg = Qwen3VLVisionConfig(hidden_size=1280, intermediate_size=5120, hidden_act=act)
+    torch.manual_seed(5)
+    mlp = Qwen3VLVisionMLP(cfg).to(torch.bfloat16).to(DEV).eval()
+    with torch.no_grad():
+        for lin in (mlp.linear_fc1, mlp.linear_fc2):
+            lin.weight.normal_(0, 0.02)
+            lin.bias.normal_(0, 0.1)
+    x = torch.randn(rows, 1280, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        ref = mlp(x)
+        assert integrate.fuse_gelu_mlps(mlp) == 1
+        kind = mlp._umic_fc[2]
+        out = mlp(x)
+        torch.cuda.synchronize()
+    assert kind == ("gelu_tanh" if act == "gelu_pytorch_tanh" else "gelu")
+    if rows < integrate.FUSE_MIN_ROWS:
+        assert call_log["umic_linear_ws_bf16"] == 0 and torch.equal(out, ref)
+    else:
+        assert call_log["umic_linear_ws_bf16"] == 1
+        assert max_rel_err(out, ref) <= TOL and rel_err(out, ref) <= TOL, (max_rel_err(out, ref),
+                                                                         rel_err(out, ref))

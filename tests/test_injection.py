@@ -154,6 +154,7 @@ def test_cpu_patched_vision_model_is_bit_identical():
         assert integrate.fuse_layernorms(m) == 4 * 2 + 1 + 1   # blocks, merger, deepstack merger
         assert integrate.fuse_vision_rope()
         assert integrate.fuse_vision_encoder_pipeline(m) == 1
+        assert integrate.fuse_gelu_mlps(m) == 4      # blocks; not the mergers
         out = m(px.to(BF), grid_thw=grid)
         out2 = m(px.to(BF), grid_thw=grid)  # cached constants path
     for o in (out, out2):
@@ -193,6 +194,72 @@ def test_fuse_min_rows_boundary(monkeypatch):
             q(x)
     assert calls == [("p5", 64), ("lin", 64)]
     assert integrate.FUSE_MIN_ROWS == 64
+
+
+def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):
+    """The ViT MLP's fc1 takes the fused linear from 64 rows, with the GELU
+    form the module computes (Qwen3-VL's ViT: gelu_pytorch_tanh)."""
+    calls = []
+
+    def fake_lin(x, w, b=None, act=None):
+        calls.append((x.reshape(-1, x.shape[-1]).shape[0], act))
+        h = nn.functional.linear(x, w, b)
+        return nn.functional.gelu(h, approximate="tanh" if act == "gelu_tanh" else "none")
+
+    monkeypatch.setattr(linear, "linear_eligible", lambda *a: True)
+    monkeypatch.setattr(linear, "linear_hip", fake_lin)
+    m = tiny_vision_model()
+    integrate.fuse_gelu_mlps(m)
+    mlp = m.blocks[0].mlp
+    for rows in (63, 64):
+        with torch.no_grad():
+            mlp(torch.randn(rows, 64).to(BF))
+    assert calls == [(64, "gelu_tanh")]
+
+
+def test_gelu_kind_by_values():
+    from transformers import activations as hf
+
+    assert integrate._gelu_kind(nn.GELU()) == "gelu"
+    assert integrate._gelu_kind(nn.GELU(approximate="tanh")) == "gelu_tanh"
+    assert integrate._gelu_kind(nn.functional.gelu) == "gelu"
+    assert integrate._gelu_kind(hf.GELUActivation()) == "gelu"
+    assert integrate._gelu_kind(hf.ACT2FN["gelu_pytorch_tanh"]) == "gelu_tanh"
+    assert integrate._gelu_kind(hf.NewGELUActivation()) == "gelu_tanh"
+    # GELU-named but another function: left to eager
+    assert integrate._gelu_kind(hf.QuickGELUActivation()) is None
+    assert integrate._gelu_kind(nn.SiLU()) is None
+    assert integrate._gelu_kind(None) is None
+
+
+class _ToyMLP(nn.Module):
+    def forward(self, x):
+        return self.fc2(self.act_fn(self.fc1(x)))
+
+
+def test_gelu_mlp_matcher_rules():
+    def mlp(d_in=32, d_hid=64, d_out=32, act=None, gate=False, names=("fc1", "fc2")):
+        m = _ToyMLP()
+        setattr(m, names[0], nn.Linear(d_in, d_hid))
+        setattr(m, names[1], nn.Linear(d_hid, d_out))
+        m.act_fn = act if act is not None else nn.GELU()
+        if gate:
+            m.gate_proj = nn.Linear(d_in, d_hid)
+        return m
+
+    assert integrate._is_gelu_mlp(mlp())[2] == "gelu"
+    assert integrate._is_gelu_mlp(mlp(names=("linear_fc1", "linear_fc2")))[2] == "gelu"
+    assert integrate._is_gelu_mlp(mlp(act=nn.GELU(approximate="tanh")))[2] == "gelu_tanh"
+    assert integrate._is_gelu_mlp(mlp(d_out=48)) is None          # patch-merger shape
+    assert integrate._is_gelu_mlp(mlp(gate=True)) is None         # a gated MLP
+    assert integrate._is_gelu_mlp(mlp(act=nn.SiLU())) is None
+    assert integrate._is_gelu_mlp(mlp(names=("w1", "w2"))) is None
+    m = mlp()
+    w = m.fc1.weight
+    assert integrate.fuse_gelu_mlps(m, dry_run=True) == 1 and "forward" not in m.__dict__
+    assert integrate.fuse_gelu_mlps(m) == 1 and m.fc1.weight is w
+    x = torch.randn(4, 32)
+    assert torch.equal(m(x), m.fc2(m.act_fn(m.fc1(x))))          # CPU: eager
 
 
 def test_gate_silu_mul_cpu_is_eager():
@@ -260,7 +327,7 @@ def test_apply_report():
     assert report["lm_rmsnorm_fused"] == 9 and report["lm_add_rmsnorm_fused"] == 2
     assert report["text_rope_fused"] is True
     assert report["ve_layernorm_fused"] == 10 and report["ve_rope_fused"] is True
-    assert report["ve_pipeline_fused"] == 1
+    assert report["ve_pipeline_fused"] == 1 and report["ve_gelu_mlp_fused"] == 4
     assert report["expert_rmsnorm_fused"] == 5 and report["expert_add_rmsnorm_fused"] == 1
     assert report["lm_kv_rope_fused"] == 2 and report["expert_kv_rope_fused"] == 1
     assert report["flow_cache_hook"] is True and report["decode_graph"] is True

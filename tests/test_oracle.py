@@ -311,6 +311,26 @@ def test_linear_gelu_vs_torch(oracle_lib):
     assert rel_err(ours, ref) < 5e-3
 
 
+def test_linear_gelu_tanh_vs_torch(oracle_lib):
+    """act 2 is torch's gelu(approximate="tanh"): close to it in float64, and
+    measurably apart from the erf form on the same inputs (|difference| up to
+    ~5e-4 near x = +-2), so swapped activation codes fail here."""
+    o = oracle_lib
+    gen = torch.Generator().manual_seed(10)
+    x, w = bf16_randn(40, 128, gen=gen), bf16_randn(64, 128, scale=0.2, gen=gen)
+    b = bf16_randn(64, scale=0.5, gen=gen)
+    pre = x.double() @ w.double().T + b.double()
+    ref_t = torch.nn.functional.gelu(pre, approximate="tanh")
+    ref_e = torch.nn.functional.gelu(pre)
+    ours = from_bits(o.linear(bits(x), bits(w), bits(b), act=2, fused=True)).double()
+    assert rel_err(ours, ref_t) < 5e-3
+    # bf16 rounding of the output is <= 2^-9 relative; the tanh/erf gap exceeds it
+    gap = (ref_t - ref_e).abs()
+    far = gap > 4 * 2.0 ** -9 * ref_t.abs() + 1e-4
+    assert far.sum() > 20
+    assert ((ours - ref_t).abs()[far] < (ours - ref_e).abs()[far]).all()
+
+
 def test_reference_smoke_formulas(oracle_lib):
     """The reference's only numeric check (scripts/check_env.py:116-171,
     seed 0, rel-err < 2e-2) restated on the oracle at a reduced row count."""

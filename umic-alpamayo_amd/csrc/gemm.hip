@@ -100,6 +100,51 @@ __device__ __forceinline__ void stage_barrier() {
 
 typedef u32x4 LdsRing[kStages][2][kBM * Geo::CPR];
 
+// Exact-erf GELU for the linear's epilogue, formed as eager does:
+// GELU(x) = 0.5 * x * (1 + erf(x / sqrt2)) in fp32.  erf(|u|) is taken as
+// 1 - erfc(|u|) rounded to fp32, with erfc(z) = t * exp(-z^2 + P(t)),
+// t = 1 / (1 + z/2) -- the functional form of Numerical Recipes' erfcc
+// (W. H. Press et al., 2nd ed., sec. 6.2).  The coefficients of P are this
+// library's own least-squares fit in float64 of log(erfc(z) / t) + z^2 on
+// z in [0, 10]; evaluated in fp32 with the hardware reciprocal and exp2,
+// erfc is within 1.5e-5 relative on [0, 10], so the fp32 erf matches a
+// correctly rounded erff to about an ulp (tests/test_gelu_epilogue.py
+// re-checks these constants).  Forming 1 + erf in fp32 keeps eager's
+// behaviour for very negative x, where it cancels to 0 or to one ulp of 1
+// (the more accurate x/2 * erfc(|u|) would differ from eager there by many
+// bf16 ulps).  About 17 VALU operations against the library erff's branches.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float z = __builtin_fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.5f * z);
+  float p = 1.449302137e-01f;
+  p = __builtin_fmaf(p, t, -6.808271779e-01f);
+  p = __builtin_fmaf(p, t, 1.156733757e+00f);
+  p = __builtin_fmaf(p, t, -6.962518993e-01f);
+  p = __builtin_fmaf(p, t, -8.028043184e-02f);
+  p = __builtin_fmaf(p, t, 1.267586182e-03f);
+  p = __builtin_fmaf(p, t, 3.460280007e-02f);
+  p = __builtin_fmaf(p, t, 3.866404121e-01f);
+  p = __builtin_fmaf(p, t, 9.986327833e-01f);
+  p = __builtin_fmaf(p, t, -1.265447997e+00f);
+  const float erfc_z = t * __builtin_amdgcn_exp2f((p - z * z) * 1.4426950408889634f);
+  const float erf_abs = 1.0f - erfc_z;
+  return 0.5f * x * (1.0f + (x < 0.0f ? -erf_abs : erf_abs));
+}
+
+// tanh-approximate GELU, as torch's gelu(approximate="tanh") (HF
+// gelu_pytorch_tanh, the Qwen3-VL ViT MLP's activation) forms it in fp32:
+// 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3) in the same
+// operation order.  tanh|y| = 1 - 2 / (1 + exp(2|y|)) with the hardware exp2
+// and reciprocal: the final subtraction puts it on the fp32 grid of [0.5, 1),
+// as tanhf's result, so 1 + tanh(y) cancels in the negative tail exactly as
+// eager's does; it is exactly 1 where exp overflows.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float y = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+  const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(y) * 2.8853900817779268f);  // exp(2|y|)
+  const float th_abs = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return 0.5f * x * (1.0f + (y < 0.0f ? -th_abs : th_abs));
+}
+
 // Tile origin of logical tile t in the grouped order: groups of kGroupM tile
 // rows, m fastest inside a group.
 __device__ __forceinline__ void tile_origin(const GemmArgs& g, int t, int bw, int& m0, int& n0) {
@@ -360,7 +405,8 @@ struct Pipe {
         x = x * __builtin_amdgcn_rcpf(den) * u[e];
       } else {
         if constexpr (BIAS) x = x + bias[e];
-        if constexpr (ACT == UMIC_ACT_GELU) x = 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+        if constexpr (ACT == UMIC_ACT_GELU) x = gelu_erf(x);
+        if constexpr (ACT == UMIC_ACT_GELU_TANH) x = gelu_tanh(x);
       }
       o[e] = x;
     }
@@ -728,7 +774,8 @@ extern "C" int umic_linear_bf16(const void* x, const void* w, const void* bias, 
                                 int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                                 int64_t ldo, int act, void* stream) {
   if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
-  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU) return UMIC_ERR_INVALID_ARG;
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
+    return UMIC_ERR_INVALID_ARG;
   if (M == 0 || N == 0) return UMIC_OK;  // empty tensors may carry null pointers
   if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
   if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
@@ -740,6 +787,9 @@ extern "C" int umic_linear_bf16(const void* x, const void* w, const void* bias, 
   hipStream_t st = as_stream(stream);
   if (act == UMIC_ACT_GELU)
     return bias ? launch_gemm<1, UMIC_ACT_GELU, true>(g, st) : launch_gemm<1, UMIC_ACT_GELU, false>(g, st);
+  if (act == UMIC_ACT_GELU_TANH)
+    return bias ? launch_gemm<1, UMIC_ACT_GELU_TANH, true>(g, st)
+                : launch_gemm<1, UMIC_ACT_GELU_TANH, false>(g, st);
   return bias ? launch_gemm<1, UMIC_ACT_NONE, true>(g, st) : launch_gemm<1, UMIC_ACT_NONE, false>(g, st);
 }
 
@@ -756,7 +806,8 @@ extern "C" int umic_linear_ws_bf16(const void* x, const void* w, const void* bia
   if (pl.bytes == 0 || workspace_bytes < pl.bytes || !workspace ||
       ((uintptr_t)workspace & 255u))  // data-parallel path
     return umic_linear_bf16(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, stream);
-  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU) return UMIC_ERR_INVALID_ARG;
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
+    return UMIC_ERR_INVALID_ARG;
   if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
   if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
   if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
@@ -767,6 +818,9 @@ extern "C" int umic_linear_ws_bf16(const void* x, const void* w, const void* bia
   if (act == UMIC_ACT_GELU)
     return bias ? launch_gemm_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
                 : launch_gemm_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
+  if (act == UMIC_ACT_GELU_TANH)
+    return bias ? launch_gemm_sk<UMIC_ACT_GELU_TANH, true>(g, pl, workspace, st)
+                : launch_gemm_sk<UMIC_ACT_GELU_TANH, false>(g, pl, workspace, st);
   return bias ? launch_gemm_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
               : launch_gemm_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
 }

@@ -29,6 +29,7 @@ UMIC_ROPE_TEXT = 0
 UMIC_ROPE_VISION = 1
 UMIC_ACT_NONE = 0
 UMIC_ACT_GELU = 1
+UMIC_ACT_GELU_TANH = 2
 
 _P, _I64, _F32, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
 

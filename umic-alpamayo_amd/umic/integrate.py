@@ -263,6 +263,105 @@ def fuse_layernorms(model: nn.Module, dry_run: bool = False) -> int:
     return count
 
 
+# ---------------------------------------------------------------------------
+# fc1 -> GELU -> fc2 MLPs (ViT blocks)
+# ---------------------------------------------------------------------------
+
+# fc1 / fc2 attribute aliases of GELU MLPs across ViT families
+# (reference integrate.py:262-263).
+_FC1_NAMES = ("fc1", "linear_fc1", "up_proj")
+_FC2_NAMES = ("fc2", "linear_fc2", "down_proj")
+
+# Probe points for _gelu_kind: where erf and tanh GELU differ by up to ~5e-4.
+_GELU_PROBE = torch.linspace(-6.0, 6.0, 241, dtype=torch.float32)
+
+
+def _gelu_kind(act) -> str | None:
+    """Which GELU `act` computes: "gelu" (erf), "gelu_tanh" or None.
+
+    The reference matches any module whose class name contains "gelu" and
+    always applies the erf form (integrate.py:284-289, kernels/linear.py:
+    83-86).  That name test also accepts QuickGELU (x * sigmoid(1.702 x)) and
+    the tanh forms, whose values differ; here the activation is evaluated on
+    fp32 CPU probe points and identified by its values instead (activations
+    hold no parameters).  The two GELU forms differ by up to ~5e-4 on the
+    probe; a module within 1e-6 of neither is not fused.
+    """
+    if act is None or not callable(act):
+        return None
+    try:
+        with torch.no_grad():
+            y = act(_GELU_PROBE.clone())
+    except Exception:  # noqa: BLE001 -- any failure means "not a plain GELU"
+        return None
+    if not isinstance(y, torch.Tensor) or y.shape != _GELU_PROBE.shape:
+        return None
+    y = y.detach().to("cpu", torch.float32)
+    for kind, approx in (("gelu", "none"), ("gelu_tanh", "tanh")):
+        ref = nn.functional.gelu(_GELU_PROBE, approximate=approx)
+        if (y - ref).abs().max().item() <= 1e-6:
+            return kind
+    return None
+
+
+def _mlp_act(module: nn.Module):
+    for attr in ("act_fn", "act", "activation_fn"):
+        act = getattr(module, attr, None)
+        if act is not None:
+            return act
+    return None
+
+
+def _is_gelu_mlp(module: nn.Module) -> tuple[nn.Linear, nn.Linear, str] | None:
+    """Structural match for fc1 -> GELU -> fc2 with no gate (reference
+    integrate.py:266-289): (fc1, fc2, GELU kind) or None.
+
+    fc1.in_features must equal fc2.out_features: a projection to another
+    width (the Qwen3-VL patch merger, fc1 in 4608, fc2 out 4096) shares the
+    names but is not a residual FFN block.
+    """
+    fc1 = next((getattr(module, n) for n in _FC1_NAMES
+                if isinstance(getattr(module, n, None), nn.Linear)), None)
+    fc2 = next((getattr(module, n) for n in _FC2_NAMES
+                if isinstance(getattr(module, n, None), nn.Linear)), None)
+    if fc1 is None or fc2 is None or hasattr(module, "gate_proj"):
+        return None
+    if fc1.in_features != fc2.out_features or fc2.in_features != fc1.out_features:
+        return None
+    kind = _gelu_kind(_mlp_act(module))
+    return None if kind is None else (fc1, fc2, kind)
+
+
+def _fused_gelu_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """fc1 + bias + GELU in one kernel (no fc1 output round trip before the
+    activation), then fc2 on the vendor BLAS (reference integrate.py:292-303)."""
+    fc1, fc2, kind = self._umic_fc
+    if _rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, fc1.weight, fc1.bias):
+        return _eager(self, x)
+    return fc2(linear.linear_hip(x, fc1.weight, fc1.bias, act=kind))
+
+
+def fuse_gelu_mlps(model: nn.Module, dry_run: bool = False) -> int:
+    """Fuse fc1 + GELU for every GELU-MLP module (the ViT block motif).
+
+    Returns:
+        Number of modules matched (and patched unless dry_run).
+    """
+    count = 0
+    for name, module in model.named_modules():
+        match = _is_gelu_mlp(module)
+        if match is None:
+            continue
+        count += 1
+        if not dry_run:
+            module._umic_fc = match
+            module.forward = _fused_gelu_mlp_forward.__get__(module)
+            logger.info("GELU MLP fused (%s): %s", match[2], name)
+    logger.info("fuse_gelu_mlps: %d module(s) %s", count,
+                "matched (dry run)" if dry_run else "patched")
+    return count
+
+
 def _add_layernorm(norm: nn.LayerNorm, x: torch.Tensor, residual: torch.Tensor):
     """(norm(residual + x), residual + x): fused when the kernel applies."""
     if (isinstance(norm, nn.LayerNorm) and len(norm.normalized_shape) == 1

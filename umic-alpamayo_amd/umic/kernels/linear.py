@@ -41,6 +41,10 @@ def linear_eligible(x: torch.Tensor, weight: torch.Tensor, bias=None) -> bool:
     return True
 
 
+_ACT_CODES = {None: _lib.UMIC_ACT_NONE, "gelu": _lib.UMIC_ACT_GELU,
+              "gelu_tanh": _lib.UMIC_ACT_GELU_TANH}
+
+
 def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
                act: str | None = None) -> torch.Tensor:
     """Compute act(x @ weight.T + bias).
@@ -49,10 +53,11 @@ def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
         x: [..., K] activations, bf16 on the GPU.
         weight: [N, K] nn.Linear weight (read in place).
         bias: optional [N].
-        act: None or "gelu" (erf GELU epilogue).
+        act: None, "gelu" (erf GELU epilogue) or "gelu_tanh" (tanh-approximate
+            GELU, torch's gelu(approximate="tanh")).
     """
     require_device(x, weight, *([bias] if bias is not None else []))
-    if act not in (None, "gelu"):
+    if act not in _ACT_CODES:
         raise ValueError(f"unsupported activation {act!r}")
     if not linear_eligible(x, weight, bias):
         raise ValueError(f"linear_hip: unsupported shape x{tuple(x.shape)} w{tuple(weight.shape)}"
@@ -69,7 +74,7 @@ def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
         ws, ws_bytes = workspace(x.device, stream, M, N, K)
         _lib.call("umic_linear_ws_bf16", x2d.data_ptr(), w.data_ptr(), _lib.ptr(b), out.data_ptr(),
                   M, N, K, ld(x2d), ld(w), N,
-                  _lib.UMIC_ACT_GELU if act == "gelu" else _lib.UMIC_ACT_NONE,
+                  _ACT_CODES[act],
                   _lib.ptr(ws), ws_bytes, stream)
     return out.reshape(*shape[:-1], N)
 
