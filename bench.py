@@ -528,8 +528,9 @@ def main() -> int:
                     help="skip the fused RoPE + KV-cache append timing")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
-              "path is row-parallel and would shard along M with no exchange, see DESIGN.md",
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the norm "
+              "and RoPE kernels would shard along M (tokens) with no exchange, and the "
+              "GEMMs by weight columns with one all-reduce after down_proj and o_proj",
               file=sys.stderr)
         return 2
 
