@@ -71,6 +71,48 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
     assert call_log["umic_linear_ws_bf16"] + call_log["umic_linear_bf16"] == 3 * gemm_calls
 
 
+def test_config1_mlp_block(call_log):
+    """BASELINE config 1 on the GPU: x[256,1024] ~N(0,1) -> RMSNorm (eps 1e-6,
+    weight 1+N(0,0.1)) -> gate/up 1024->3072 (no bias, N(0,0.02)) ->
+    SiLU(gate)*up -> down 3072->1024, built from transformers' Qwen3-VL text
+    modules and seeded in that order.  Fused against the unpatched block, the
+    fused gate_silu_mul against the oracle (one rounding of the fp32 product),
+    and every fused site counted."""
+    import numpy as np
+    from helpers import bits, ulp
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextMLP,
+                                                                Qwen3VLTextRMSNorm)
+
+    import oracle
+
+    cfg = Qwen3VLTextConfig(hidden_size=1024, intermediate_size=3072, rms_norm_eps=1e-6)
+    norm, mlp = Qwen3VLTextRMSNorm(1024, eps=1e-6), Qwen3VLTextMLP(cfg)
+    torch.manual_seed(0)
+    x = torch.randn(256, 1024)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(1024))
+        for lin in (mlp.gate_proj, mlp.up_proj, mlp.down_proj):
+            lin.weight.normal_(0, 0.02)
+    block = torch.nn.Sequential(norm, mlp).to(torch.bfloat16).to(DEV).eval()
+    x = x.to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        ref = block(x)
+        assert integrate.fuse_rmsnorms(block) == 1 and integrate.fuse_mlps(block) == 1
+        out = block(x)
+        h = norm(x)
+        from umic.kernels import fused_ffn
+        p5 = fused_ffn.gate_silu_mul_hip(h, mlp.gate_proj.weight.t(), mlp.up_proj.weight.t())
+        torch.cuda.synchronize()
+    assert max_rel_err(out, ref) <= TOL and rel_err(out, ref) <= TOL, (max_rel_err(out, ref),
+                                                                     rel_err(out, ref))
+    want = oracle.gate_silu_mul(bits(h), bits(mlp.gate_proj.weight), bits(mlp.up_proj.weight))
+    d = ulp(bits(p5), want)
+    assert (d <= 1).mean() > 0.999, np.bincount(d.ravel())[:8]
+    assert call_log["umic_rmsnorm_bf16"] == 2             # the block's norm, then h
+    assert call_log["umic_gate_silu_mul_bf16"] == 2       # the block's MLP, then p5
+
+
 def test_vision_pipeline_on_gpu(call_log):
     from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
     from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionModel
