@@ -73,6 +73,7 @@ class UmicKernelError(RuntimeError):
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 _load_error: str | None = None
+_fns: dict[str, object] = {}   # entry-point name -> ctypes function of _lib
 HAS_KERNELS = False
 
 
@@ -93,6 +94,7 @@ def load(path: str | None = None) -> ctypes.CDLL:
             fn.argtypes = args
             fn.restype = RESTYPES.get(name, _I)
         _lib = lib
+        _fns.clear()
         HAS_KERNELS = True
         return lib
 
@@ -124,7 +126,10 @@ def error_string(code: int) -> str:
 
 def call(name: str, *args) -> None:
     """Invoke entry point ``name``; raise UmicKernelError on non-zero status."""
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != UMIC_OK:
         raise UmicKernelError(name, rc, error_string(rc))
 
@@ -133,8 +138,16 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# torch's accessor for the raw handle of a device's current stream (what
+# torch.cuda.current_stream(dev).cuda_stream returns, without building a
+# Stream object: ~0.1 us against ~2 us per call); the public path otherwise.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """hipStream_t handle of the current torch stream on t's device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
