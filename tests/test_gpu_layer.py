@@ -71,6 +71,37 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
     assert call_log["umic_linear_ws_bf16"] + call_log["umic_linear_bf16"] == 3 * gemm_calls
 
 
+def test_decoder_layer_with_autograd_runs_eager(call_log):
+    """Grad mode on and weights requiring grad: the patched layer makes no
+    kernel call (the kernels have no backward) and equals the unpatched layer
+    bit for bit.  Only the forward runs here; SDPA is held to its flash and
+    memory-efficient kernels."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    layer, rot = decoder_layer()
+    torch.manual_seed(2)
+    h = torch.randn(1, 256, 4096).to(torch.bfloat16).to(DEV)
+    pos = torch.arange(256, device=DEV)[None]
+    with torch.no_grad():
+        cos_sin = rot(h, pos)
+    assert layer.mlp.gate_proj.weight.requires_grad
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        ref = layer(h, position_embeddings=cos_sin)
+        integrate.fuse_mlps(layer)
+        integrate.fuse_linears(layer)
+        integrate.fuse_rmsnorms(layer)
+        integrate.fuse_add_rmsnorm(layer)
+        assert integrate.fuse_text_rope()
+        out = layer(h, position_embeddings=cos_sin)
+        torch.cuda.synchronize()
+        assert out.requires_grad and torch.equal(out, ref)
+        assert sum(call_log.values()) == 0, dict(call_log)
+        with torch.no_grad():
+            layer(h, position_embeddings=cos_sin)
+        torch.cuda.synchronize()
+    assert call_log["umic_gate_silu_mul_bf16"] == 1 and call_log["umic_rope_qk_bf16"] == 1
+
+
 def test_config1_mlp_block(call_log):
     """BASELINE config 1 on the GPU: x[256,1024] ~N(0,1) -> RMSNorm (eps 1e-6,
     weight 1+N(0,0.1)) -> gate/up 1024->3072 (no bias, N(0,0.02)) ->

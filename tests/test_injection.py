@@ -217,6 +217,55 @@ def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):
     assert calls == [(64, "gelu_tanh")]
 
 
+def test_autograd_keeps_the_eager_path(monkeypatch):
+    """The kernels have no backward: with grad mode on and weights that
+    require grad, every GEMM and norm site runs the class forward (autograd
+    records eager's graph); under no_grad the same calls take the kernels."""
+    from umic.kernels import rmsnorm
+
+    calls = []
+
+    def fake_p5(x, wg_kn, wu_kn):
+        calls.append("p5")
+        return fused_ffn.gate_silu_mul_eager(x, wg_kn, wu_kn)
+
+    def fake_lin(x, w, b=None, act=None):
+        calls.append("lin")
+        return nn.functional.linear(x, w, b)
+
+    def fake_rms(x, w, eps):
+        calls.append("rms")
+        return x
+
+    monkeypatch.setattr(fused_ffn, "p5_eligible", lambda *a: True)
+    monkeypatch.setattr(fused_ffn, "gate_silu_mul_hip", fake_p5)
+    monkeypatch.setattr(linear, "linear_eligible", lambda *a: True)
+    monkeypatch.setattr(linear, "linear_hip", fake_lin)
+    monkeypatch.setattr(rmsnorm, "rmsnorm_eligible", lambda *a: True)
+    monkeypatch.setattr(rmsnorm, "rmsnorm_hip", fake_rms)
+    m = tiny_text_model(layers=1)
+    integrate.fuse_mlps(m)
+    integrate.fuse_linears(m)
+    integrate.fuse_rmsnorms(m)
+    mlp, q, norm = m.layers[0].mlp, m.layers[0].self_attn.q_proj, m.norm
+    x = torch.randn(1, 64, 128).to(BF)
+    assert mlp.gate_proj.weight.requires_grad
+    out = mlp(x)
+    q(x)
+    norm(x)
+    assert calls == [] and out.requires_grad
+    out.float().sum().backward()
+    assert mlp.gate_proj.weight.grad is not None
+    with torch.no_grad():
+        mlp(x)
+        q(x)
+        norm(x)
+    assert calls == ["p5", "lin", "rms"]
+    with torch.inference_mode():
+        norm(x)
+    assert calls[-1] == "rms" and len(calls) == 4
+
+
 def test_gelu_kind_by_values():
     from transformers import activations as hf
 

@@ -11,9 +11,10 @@ hooks, and deleting the attribute restores the class forward.
 
 Each replacement forward first decides whether the fused gfx950 kernel
 reproduces the module on the given inputs (GPU bf16 tensors of a handled
-layout; for the GEMM sites also at least FUSE_MIN_ROWS rows).  If not, it
-runs the module's own class forward -- the original eager math on whatever
-device the inputs live on.  If the inputs are eligible but libumic_hip.so
+layout; for the GEMM sites also at least FUSE_MIN_ROWS rows; and no
+gradient to carry, since the kernels have no backward).  If not, it runs
+the module's own class forward -- the original eager math on whatever
+device the inputs live on, recorded by autograd as usual.  If the inputs are eligible but libumic_hip.so
 is missing, the kernel wrapper raises: the fused path never degrades
 silently.
 """
@@ -26,6 +27,7 @@ import torch
 from torch import nn
 
 from umic.kernels import fused_ffn, layernorm, linear, rmsnorm, rope
+from umic.kernels._common import grad_needed
 
 logger = logging.getLogger(__name__)
 
@@ -88,7 +90,8 @@ def _is_p5_mlp(module: nn.Module) -> bool:
 def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """P5-fused replacement: silu(x@Wg)*(x@Wu) in one kernel, then down."""
     wg, wu = self.gate_proj.weight, self.up_proj.weight
-    if _rows(x) < FUSE_MIN_ROWS or not fused_ffn.p5_eligible(x, wg, wu):
+    if (_rows(x) < FUSE_MIN_ROWS or not fused_ffn.p5_eligible(x, wg, wu)
+            or grad_needed(x, wg, wu)):
         return _eager(self, x)
     # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
     # takes -- the kernel reads the original weight memory.
@@ -124,7 +127,8 @@ def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
 
 def _patched_linear_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
     """Route large-M calls to the fused linear; GEMV stays on the vendor BLAS."""
-    if _rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, self.weight, self.bias):
+    if (_rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, self.weight, self.bias)
+            or grad_needed(x, self.weight, self.bias)):
         return _eager(self, x)
     return linear.linear_hip(x, self.weight, self.bias)
 
@@ -154,7 +158,7 @@ def fuse_linears(model: nn.Module, names: tuple[str, ...] = INEFFICIENT_LINEAR_N
 
 def _patched_rmsnorm_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """One fused kernel replacing the eager pow/mean/rsqrt/mul/cast chain."""
-    if not rmsnorm.rmsnorm_eligible(x, self.weight):
+    if not rmsnorm.rmsnorm_eligible(x, self.weight) or grad_needed(x, self.weight):
         return _eager(self, x)
     return rmsnorm.rmsnorm_hip(x, self.weight, _norm_eps(self))
 
@@ -194,7 +198,8 @@ def _add_rmsnorm(norm: nn.Module, x: torch.Tensor, residual: torch.Tensor):
     w = getattr(norm, "weight", None)
     if ("rmsnorm" in type(norm).__name__.lower() and isinstance(w, torch.Tensor)
             and x.shape == residual.shape and residual.dtype == x.dtype
-            and rmsnorm.rmsnorm_eligible(x, w) and residual.device == x.device):
+            and rmsnorm.rmsnorm_eligible(x, w) and residual.device == x.device
+            and not grad_needed(x, residual, w)):
         return rmsnorm.add_rmsnorm_hip(x, residual, w, _norm_eps(norm))
     summed = residual + x
     return norm(summed), summed
@@ -244,7 +249,8 @@ def fuse_add_rmsnorm(model: nn.Module, dry_run: bool = False) -> int:
 
 def _patched_layernorm_forward(self: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
     """One fused kernel replacing eager's LayerNorm."""
-    if not layernorm.layernorm_eligible(x, self.weight, self.bias):
+    if (not layernorm.layernorm_eligible(x, self.weight, self.bias)
+            or grad_needed(x, self.weight, self.bias)):
         return _eager(self, x)
     return layernorm.layernorm_hip(x, self.weight, self.bias, self.eps)
 
@@ -336,7 +342,8 @@ def _fused_gelu_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """fc1 + bias + GELU in one kernel (no fc1 output round trip before the
     activation), then fc2 on the vendor BLAS (reference integrate.py:292-303)."""
     fc1, fc2, kind = self._umic_fc
-    if _rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, fc1.weight, fc1.bias):
+    if (_rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, fc1.weight, fc1.bias)
+            or grad_needed(x, fc1.weight, fc1.bias)):
         return _eager(self, x)
     return fc2(linear.linear_hip(x, fc1.weight, fc1.bias, act=kind))
 
@@ -367,7 +374,8 @@ def _add_layernorm(norm: nn.LayerNorm, x: torch.Tensor, residual: torch.Tensor):
     if (isinstance(norm, nn.LayerNorm) and len(norm.normalized_shape) == 1
             and x.shape == residual.shape and residual.dtype == x.dtype
             and residual.device == x.device
-            and layernorm.layernorm_eligible(x, norm.weight, norm.bias)):
+            and layernorm.layernorm_eligible(x, norm.weight, norm.bias)
+            and not grad_needed(x, residual, norm.weight, norm.bias)):
         return layernorm.add_layernorm_hip(x, residual, norm.weight, norm.bias, norm.eps)
     summed = residual + x
     return norm(summed), summed
@@ -432,6 +440,11 @@ def _fused_vision_encoder_forward(self: nn.Module, hidden_states: torch.Tensor,
     h = h + attn(norm1(h)); h = h + mlp(norm2(h)) (modeling_qwen3_vl.py:
     299-306); each fused add is that same bf16 add.
     """
+    if torch.is_grad_enabled() and (hidden_states.requires_grad or any(
+            p.requires_grad for p in self.parameters())):
+        # the cached constants are detached: with autograd live, the class
+        # forward (whose submodules still take their own eager fallbacks)
+        return type(self).forward(self, hidden_states, grid_thw, **kwargs)
     cache: dict = self._umic_ve_cache
     key = tuple(grid_thw.reshape(-1).tolist())
     if cache.get("key") != key:
@@ -625,7 +638,9 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
     if isinstance(past_key_values, InplaceKVCache) and self.layer_idx < len(
             past_key_values.layers):
         layer = past_key_values.layers[self.layer_idx]
-    if not isinstance(layer, InplaceLayer) or self.training:
+    if (not isinstance(layer, InplaceLayer) or self.training
+            or grad_needed(hidden_states, self.q_proj.weight, self.k_proj.weight,
+                           self.v_proj.weight)):
         return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
                                   past_key_values=past_key_values, **kwargs)
     input_shape = hidden_states.shape[:-1]

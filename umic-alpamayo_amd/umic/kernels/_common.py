@@ -26,6 +26,18 @@ def require_device(*tensors: torch.Tensor) -> None:
     _lib.lib()  # raises UmicLibraryError if libumic_hip.so is unavailable
 
 
+def grad_needed(*tensors) -> bool:
+    """True when autograd would have to flow through a fused op: grad mode is
+    on and some participating tensor requires grad.  The kernels have no
+    backward, so such calls take the eager path and autograd records the
+    same graph as without UMIC.  Under ``torch.no_grad()`` or
+    ``torch.inference_mode()`` (the inference setting) this is one mode check.
+    """
+    if not torch.is_grad_enabled():
+        return False
+    return any(t is not None and t.requires_grad for t in tensors)
+
+
 def rows2d(x: torch.Tensor) -> torch.Tensor:
     """[..., n] -> [rows, n] view with unit inner stride (copy only if needed)."""
     x2d = x.reshape(-1, x.shape[-1])

@@ -23,7 +23,7 @@ import inspect
 import torch
 
 from umic import _lib
-from umic.kernels._common import require_device
+from umic.kernels._common import grad_needed, require_device
 
 MAX_HEAD_DIM = 1024  # cos/sin rows of a block's positions are staged in LDS
 
@@ -150,7 +150,8 @@ def make_text_rope(fallback):
     unsq = _unsqueeze_dim_of(fallback)
 
     def apply_rotary_text(q, k, cos, sin, *args, **kwargs):
-        if text_rope_eligible(q, k, cos, sin, unsq(args, kwargs)):
+        if (text_rope_eligible(q, k, cos, sin, unsq(args, kwargs))
+                and not grad_needed(q, k, cos, sin)):
             require_device(q, k, cos, sin)
             return _rope(q, k, cos, sin, _lib.UMIC_ROPE_TEXT, "bhsd")
         return fallback(q, k, cos, sin, *args, **kwargs)
@@ -163,7 +164,8 @@ def make_vision_rope(fallback):
     """Drop-in for HF apply_rotary_pos_emb_vision with an eager fallback."""
 
     def apply_rotary_vision(q, k, cos, sin, *args, **kwargs):
-        if not args and not kwargs and vision_rope_eligible(q, k, cos, sin):
+        if (not args and not kwargs and vision_rope_eligible(q, k, cos, sin)
+                and not grad_needed(q, k, cos, sin)):
             require_device(q, k)
             return _rope(q, k, cos, sin, _lib.UMIC_ROPE_VISION, "shd")
         return fallback(q, k, cos, sin, *args, **kwargs)
