@@ -32,7 +32,9 @@ Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
 six fused norm/RoPE kernels (algorithmic bytes / summed durations);
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
 (by time) of the step; cpu_baseline = the CPU oracle (scalar C, one core)
-timed on a bounded sample of the same norm/RoPE workload, in GB/s.
+timed on a bounded sample of the same norm/RoPE workload, in GB/s;
+cpu_eager = the reference's own CPU path (HF's eager modules and RoPE
+functions in torch, all host threads) on the same sample.
 layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
 prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
 HIP graph); --no-layer skips it.  kv_cache = text RoPE fused with the
@@ -209,6 +211,62 @@ def cpu_baseline(sample_s: float) -> dict:
             "sample": f"{passes} pass(es) of the six norm/RoPE oracle functions on 1/4 of the "
                       f"BASELINE rows ({tot_b / passes / 1e6:.0f} MB per pass), "
                       f"{tot_t:.1f} s of single-thread scalar C"}
+
+
+def cpu_eager(sample_s: float) -> dict:
+    """The reference's own CPU path: its eager fallback, i.e. HF transformers'
+    Qwen3-VL RMSNorm module, nn.LayerNorm, the residual adds and HF's
+    apply_rotary_pos_emb / apply_rotary_pos_emb_vision, run by torch on the
+    host cores in bf16 (fp32 tables for vision, as HF builds them) on the same
+    quarter-row sample as cpu_baseline, bytes counted as for the GPU kernels."""
+    import torch
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as hf
+
+    gen = torch.Generator().manual_seed(0)
+
+    def bfr(*shape, scale=1.0, shift=0.0):
+        return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16)
+
+    M, H, MV, HV, D = 3100 // 4, 4096, 16384 // 4, 1280, 128
+    x, r = bfr(M, H), bfr(M, H)
+    rms = hf.Qwen3VLTextRMSNorm(H, eps=1e-6)
+    xv, rv = bfr(MV, HV), bfr(MV, HV)
+    ln = torch.nn.LayerNorm(HV, eps=1e-6)
+    with torch.no_grad():
+        rms.weight.copy_(bfr(H, scale=0.1, shift=1.0).float())
+        ln.weight.copy_(bfr(HV, scale=0.1, shift=1.0).float())
+        ln.bias.copy_(bfr(HV, scale=0.1).float())
+    rms, ln = rms.to(torch.bfloat16), ln.to(torch.bfloat16)
+    q, k = bfr(1, M, 32, D).transpose(1, 2), bfr(1, M, 8, D).transpose(1, 2)
+    ct, st = bfr(1, M, D), bfr(1, M, D)
+    vq, vk = bfr(MV, 16, 80), bfr(MV, 16, 80)
+    cv, sv = torch.randn(MV, 80, generator=gen), torch.randn(MV, 80, generator=gen)
+    work = [
+        (lambda: rms(x), 4 * M * H),
+        (lambda: rms(x + r), 8 * M * H),
+        (lambda: ln(xv), 4 * MV * HV),
+        (lambda: ln(xv + rv), 8 * MV * HV),
+        (lambda: hf.apply_rotary_pos_emb(q, k, ct, st), 4 * 40 * M * D + 4 * M * D),
+        (lambda: hf.apply_rotary_pos_emb_vision(vq, vk, cv, sv), 4 * 32 * MV * 80 + 8 * MV * 80),
+    ]
+    tot_b, tot_t, passes = 0, 0.0, 0
+    with torch.no_grad():
+        for fn, _ in work:   # first-call setup out of the timing
+            fn()
+        t_end = time.perf_counter() + sample_s
+        while time.perf_counter() < t_end or passes == 0:
+            for fn, nbytes in work:
+                t0 = time.perf_counter()
+                fn()
+                tot_t += time.perf_counter() - t0
+                tot_b += nbytes
+            passes += 1
+    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "reference eager (torch CPU)",
+            "sample": f"{passes} pass(es) of HF's eager RMSNorm, add+RMSNorm, LayerNorm, "
+                      f"add+LayerNorm, text and vision RoPE on 1/4 of the BASELINE rows "
+                      f"({tot_b / passes / 1e6:.0f} MB per pass), {tot_t:.1f} s, bf16 on "
+                      f"{torch.get_num_threads()} threads"}
 
 
 def load_traffic(name: str):
@@ -628,6 +686,7 @@ def main() -> int:
         "layer": None if args.no_layer else layer_step(),
         "kv_cache": None if args.no_kv_cache else kv_cache_step(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_s),
+        "cpu_eager": None if args.no_cpu_baseline else cpu_eager(args.cpu_sample_s / 2),
     }
     print(json.dumps(out), flush=True)
     return 0
