@@ -392,6 +392,22 @@ def test_apply_report():
     integrate.unfuse_rope()
 
 
+def test_apply_twice_is_idempotent():
+    """A second apply() patches nothing new: same report, one cache hook per
+    module, one decode-graph runner."""
+    model = _wrap(lm=tiny_text_model(), visual=tiny_vision_model(),
+                  expert=tiny_text_model(layers=1))
+    first = optimize.apply(model)
+    runner = model.vlm.forward._umic_runner
+    hooks = len(model.expert._forward_pre_hooks)
+    second = optimize.apply(model)
+    assert second == first
+    assert model.vlm.forward._umic_runner is runner
+    assert runner.orig_forward.__self__ is model.vlm
+    assert len(model.expert._forward_pre_hooks) == hooks == 1
+    integrate.unfuse_rope()
+
+
 def test_find_lm_module_variants():
     lm = tiny_text_model(layers=1)
     assert optimize.find_lm_module(_wrap(lm=lm)) is lm

@@ -75,6 +75,7 @@ class DecodeGraphRunner:
         def forward(*args: Any, **kwargs: Any):
             return self(*args, **kwargs)
 
+        forward._umic_runner = self
         vlm.forward = forward
         orig_generate = getattr(vlm, "generate", None)
         if orig_generate is not None:
@@ -228,7 +229,13 @@ class DecodeGraphRunner:
 
 def fuse_decode_graph(vlm: torch.nn.Module, max_new_tokens: int = 96) -> DecodeGraphRunner:
     """Install the per-length decode graph runner on the VLM
-    (src/umic/graph.py:179-181)."""
+    (src/umic/graph.py:179-181).  Idempotent: a VLM that already carries a
+    runner keeps it (a second one would wrap the first and keep a second KV
+    cache)."""
+    existing = getattr(getattr(vlm, "forward", None), "_umic_runner", None)
+    if isinstance(existing, DecodeGraphRunner):
+        existing.max_new = max(existing.max_new, max_new_tokens)
+        return existing
     return DecodeGraphRunner(vlm, max_new_tokens=max_new_tokens)
 
 

@@ -700,6 +700,8 @@ def fuse_repeat_cache(repeat_module: nn.Module, extra_tokens_hint: int = 64) -> 
 
     from umic.cache import InplaceKVCache
 
+    if getattr(repeat_module, "_umic_repeat_cache_hook", None) is not None:
+        return                                   # installed already: idempotent
     state: dict[str, object] = {"orig_id": None, "converted": None}
 
     def _pre_hook(module, args, kwargs):
@@ -723,7 +725,8 @@ def fuse_repeat_cache(repeat_module: nn.Module, extra_tokens_hint: int = 64) -> 
         kwargs["past_key_values"] = conv
         return args, kwargs
 
-    repeat_module.register_forward_pre_hook(_pre_hook, with_kwargs=True)
+    repeat_module._umic_repeat_cache_hook = repeat_module.register_forward_pre_hook(
+        _pre_hook, with_kwargs=True)
     logger.info("fuse_repeat_cache: hook installed on %s", type(repeat_module).__name__)
 
 
