@@ -158,6 +158,10 @@ int umic_rope_kv_append_bf16(const void* q, const void* k, const void* v,
  * out = act(x @ w^T + bias), bf16 in/out, fp32 accumulation on MFMA.
  * x: [M, K] row stride ldx; w: [N, K] (nn.Linear layout) row stride ldw;
  * bias: [N] bf16 or NULL; out: [M, N] row stride ldo.
+ * act: UMIC_ACT_NONE, UMIC_ACT_GELU (the reference's act="gelu") or
+ * UMIC_ACT_GELU_TANH (no counterpart in the reference: the tanh GELU of the
+ * Qwen3-VL ViT MLP); the bias add and the activation run in fp32 on the
+ * accumulator, one bf16 rounding.  Any other act: UMIC_ERR_INVALID_ARG.
  * Requires K % 32 == 0, N % 8 == 0, ldx/ldw/ldo % 8 == 0 and 16-byte
  * aligned pointers (else UMIC_ERR_UNSUPPORTED).
  * Replaces: kernels/linear.py:118-145 (linear_triton), kernel
