@@ -54,6 +54,16 @@ def test_linear_bias_gelu_vs_oracle():
         _check_vs_oracle(y, oracle.linear(bits(x), bits(w), bits(b), code, fused=True))
 
 
+@pytest.mark.parametrize("act,code", [("gelu", 1), ("gelu_tanh", 2)])
+def test_linear_gelu_without_bias_vs_oracle(act, code):
+    g = torch.Generator().manual_seed(21)
+    M, N, K = 333, 264, 256
+    x, w = bf16_randn(M, K, gen=g), bf16_randn(N, K, scale=0.1, gen=g)
+    y = linear.linear_hip(x.to(DEV), w.to(DEV), None, act=act)
+    torch.cuda.synchronize()
+    _check_vs_oracle(y, oracle.linear(bits(x), bits(w), None, code, fused=True))
+
+
 def test_linear_strided_x_and_leading_dims():
     g = torch.Generator().manual_seed(4)
     big = bf16_randn(2, 70, 512 + 64, gen=g)
