@@ -8,7 +8,6 @@ paths return without touching the device).
 
 from __future__ import annotations
 
-import ctypes
 import os
 import re
 
