@@ -95,3 +95,34 @@ def test_fused_kernels_replay_in_hip_graph():
         torch.cuda.synchronize()
         for name, ref in eager.items():
             assert torch.equal(captured[name], ref), (seed, name)
+
+
+def test_stream_k_workspace_outlives_a_captured_graph():
+    """A graph captured with the stream-K linear keeps its workspace address.
+    A later, larger eager call grows the per-stream workspace; the old buffer
+    must stay allocated, so a tensor allocated afterwards is not overwritten
+    when the graph replays, and the replay still computes the same product."""
+    g = torch.Generator().manual_seed(7)
+    xs = bf16_randn(300, 12288, gen=g).to(DEV)
+    ws_ = bf16_randn(264, 12288, scale=0.02, gen=g).to(DEV)
+    xb = bf16_randn(3100, 12288, gen=g).to(DEV)
+    wb = bf16_randn(4096, 12288, scale=0.02, gen=g).to(DEV)
+    assert linear.stream_k_planned(xs, ws_) and linear.stream_k_planned(xb, wb)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ref = linear.linear_hip(xs, ws_)          # allocates this stream's workspace
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = linear.linear_hip(xs, ws_)
+        big = linear.linear_hip(xb, wb)           # grows the workspace
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    small_bytes = linear._lib.lib().umic_linear_workspace_bytes(300, 264, 12288)
+    sentinel = torch.full((small_bytes,), 0x5A, dtype=torch.uint8, device=DEV)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert bool((sentinel == 0x5A).all())
+    assert big.shape == (3100, 4096)

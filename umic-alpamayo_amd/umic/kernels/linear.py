@@ -94,16 +94,27 @@ def stream_k_planned(x: torch.Tensor, weight: torch.Tensor) -> bool:
 # is created, and reused by every later call on that stream (calls on one
 # stream never overlap).
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+# Workspaces replaced by a larger one stay allocated: a HIP graph captured
+# earlier still holds the old address, and its replays must not write into
+# memory the caching allocator has handed to another tensor.  Growth at
+# least doubles, so few are ever retired.
+_RETIRED: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, stream: int, M: int, N: int, K: int):
-    """(tensor, bytes) the stream-K linear needs for this shape, or (None, 0)."""
+    """(tensor, bytes) the stream-K linear needs for this shape, or (None, 0).
+
+    One zeroed workspace per (device, stream): the kernel leaves its counters
+    at zero after every call, and calls on one stream never overlap."""
     need = _lib.lib().umic_linear_workspace_bytes(M, N, K)
     if need <= 0:
         return None, 0
     key = (device.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _RETIRED.append(ws)
+            need = max(need, 2 * ws.numel())
         ws = torch.zeros(need, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws, ws.numel()
