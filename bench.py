@@ -56,6 +56,9 @@ for _p in (ROOT, os.path.join(ROOT, "umic-alpamayo_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+# the reference's norm / RoPE kernels, whose whole-job HBM throughput is `value`
+VALUE_SITES = ("rmsnorm", "add_rmsnorm", "layernorm", "add_layernorm", "rope_text",
+               "rope_vision")
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "fused-kernel HBM GB/s (% of peak) + LM MLP prefill ms at M=3100 bf16"
 
@@ -123,6 +126,7 @@ def build_workload():
     wu = _bf(12288, H, scale=0.02, gen=g)
     wd = _bf(H, 12288, scale=0.02, gen=g)
     hmid = _bf(M, 12288, gen=g)
+    qn_w, kn_w = _bf(D, scale=0.1, shift=1.0, gen=g), _bf(D, scale=0.1, shift=1.0, gen=g)
     eps = 1e-6
 
     def pick(r, i):
@@ -146,6 +150,11 @@ def build_workload():
         ("rope_text", lambda i: rope.apply_rotary_text_hip(*pick(rope_qk, i), cos_t, sin_t),
          2 * b2 * (32 + 8) * M * D + 2 * b2 * M * D, 0, "hbm"),
         ("rope_vision", vision, 2 * b2 * 2 * 16 * MV * 80 + 2 * 4 * MV * 80, 0, "hbm"),
+        # the attention's q_norm / k_norm fused into the text RoPE (not one of
+        # the reference's kernels: reported, not part of `value`)
+        ("qk_norm_rope", lambda i: rope.qk_norm_rope(*pick(rope_qk, i), cos_t, sin_t, qn_w, kn_w,
+                                                     eps),
+         2 * b2 * (32 + 8) * M * D + 2 * b2 * M * D + 2 * b2 * D, 0, "hbm"),
         ("q_proj", lambda i: linear.linear_hip(xg, wq), (M * H + H * H + M * H) * b2,
          2 * M * H * H, "mfma"),
         ("o_proj", lambda i: linear.linear_hip(xg, wo), (M * H + H * H + M * H) * b2,
@@ -159,7 +168,7 @@ def build_workload():
     ]
     rings = {"rmsnorm": len(rms_x), "add_rmsnorm": len(add_xr), "layernorm": len(ln_x),
              "add_layernorm": len(addln_xr), "rope_text": len(rope_qk),
-             "rope_vision": len(rope_qkv)}
+             "rope_vision": len(rope_qkv), "qk_norm_rope": len(rope_qk)}
     spacer = lambda: fused_ffn.gate_silu_mul_hip(xg, wg.t(), wu.t())  # noqa: E731
     return ents, rings, spacer
 
@@ -377,7 +386,8 @@ def layer_step() -> dict:
     """one Qwen3-VL text decoder layer (hidden 4096, 32 q /
     8 kv heads, head_dim 128, intermediate 12288, random N(0, 0.02) weights,
     norms 1 + N(0, 0.1)) timed eager and with the fused path injected
-    (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope):
+    (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope,
+    fuse_kv_rope -- with no cache, q_norm / k_norm / RoPE in one launch):
     prefill at M=3100 and decode at M=1, the decode step also captured in a
     HIP graph (torch.cuda.CUDAGraph) and replayed, as the reference's decode
     runner does (src/umic/graph.py:155-167)."""
@@ -429,6 +439,7 @@ def layer_step() -> dict:
         integrate.fuse_rmsnorms(layer)
         integrate.fuse_add_rmsnorm(layer)
         integrate.fuse_text_rope()
+        integrate.fuse_kv_rope(layer)
         try:
             res["prefill_M3100_umic_ms"] = round(timed(run[3100], 10) / 1e3, 4)
             res["decode_M1_umic_us"] = round(timed(run[1], 200), 1)
@@ -562,6 +573,19 @@ def vit_sites() -> int:
         print(json.dumps({"site": site, "M": M, "K": K, "N": N, "act": act,
                           "umic_us": round(ours, 1), "vendor_us": round(vendor, 1),
                           "umic_tflops": round(2 * M * N * K / ours / 1e6, 1)}), flush=True)
+    # the whole ViT MLP block as fuse_gelu_mlps runs it (fc1 + bias + GELU in
+    # one launch, fc2 on the vendor library) against the eager block
+    H, I = 1280, 5120
+    x = _bf(M, H)
+    w1, b1 = _bf(I, H, scale=0.02), _bf(I, scale=0.1)
+    w2, b2 = _bf(H, I, scale=0.02), _bf(H, scale=0.1)
+    for act in ("gelu_tanh", "gelu"):
+        ours = timed(lambda: F.linear(linear.linear_hip(x, w1, b1, act=act), w2, b2))
+        eager = timed(lambda: F.linear(F.gelu(F.linear(x, w1, b1), approximate=approx[act]),
+                                       w2, b2))
+        print(json.dumps({"site": f"mlp_block_{act}", "M": M, "hidden": H, "intermediate": I,
+                          "umic_us": round(ours, 1), "eager_us": round(eager, 1),
+                          "speedup": round(eager / ours, 3)}), flush=True)
     return 0
 
 
@@ -645,7 +669,7 @@ def main() -> int:
             rec["frac"] = round(rec["tflops"] / BF16_PEAK_TFLOPS, 4)
         kern[name] = rec
 
-    hbm = [k for k in kern.values() if k["bound"] == "hbm"]
+    hbm = [kern[n] for n in VALUE_SITES]
     agg = sum(k["bytes"] for k in hbm) / (sum(k["us"] for k in hbm) * 1e-6) / 1e9
     mlp_ms = (kern["gate_silu_mul"]["us"] + kern["down_proj"]["us"]) / 1e3
     dom_name = max((n for n in kern if n != "down_proj_vendor"), key=lambda n: kern[n]["us"])

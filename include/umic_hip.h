@@ -149,6 +149,55 @@ int umic_rope_kv_append_bf16(const void* q, const void* k, const void* v,
                              int64_t pos, const int64_t* pos_dev,
                              int64_t cs_sb, int64_t cs_ss, void* stream);
 
+/*
+ * The text attention's per-head RMSNorm (q_norm, k_norm) fused into the text
+ * RoPE: each head row of q and k is normalised,
+ *   y = bf16( w * bf16( x * rsqrt(mean(x^2) + eps) ) )   (HF
+ *   Qwen3VLTextRMSNorm, the umic_rmsnorm_bf16 numerics, w = q_w or k_w, [D]),
+ * then rotated as umic_rope_qk_bf16 in UMIC_ROPE_TEXT mode, in one launch:
+ * q and k are read once and written once.  Same arguments as
+ * umic_rope_qk_bf16 (TEXT mode, bf16 cos/sin) plus the two norm weights and
+ * eps.  Requires D/16 to be a power of two up to 64 (D in 16..1024), every
+ * stride a multiple of 8 elements and 16-byte aligned pointers, weights
+ * included (else UMIC_ERR_UNSUPPORTED).  Results are bit-identical to
+ * umic_rmsnorm_bf16 on each head row followed by umic_rope_qk_bf16.
+ * Replaces: the q_norm / k_norm forwards (integrate.py:134-141 on the
+ * q_norm / k_norm modules of HF Qwen3VLTextAttention) followed by
+ * kernels/rope.py:86-107 (make_text_rope) -- three launches.
+ */
+int umic_qk_rmsnorm_rope_bf16(const void* q, const void* k, void* q_out, void* k_out,
+                              const void* q_w, const void* k_w, float eps,
+                              const void* cos, const void* sin,
+                              int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+                              int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                              int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                              int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                              int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                              int64_t cs_sb, int64_t cs_ss, void* stream);
+
+/*
+ * umic_rope_kv_append_bf16 with the q / k head-row RMSNorm of
+ * umic_qk_rmsnorm_rope_bf16 applied before the rotation (v is copied
+ * unchanged): the text attention's q_norm, k_norm, RoPE and in-place cache
+ * append in one launch.  Arguments as umic_rope_kv_append_bf16, with the
+ * norm weights (q_w, k_w: [D] bf16, 16-byte aligned) and eps after sin; the
+ * same shape rules as both.
+ * Replaces: the q_norm / k_norm forwards, kernels/rope.py:86-107 and the
+ * cache append of cache.py:50-80.
+ */
+int umic_qk_rmsnorm_rope_kv_append_bf16(const void* q, const void* k, const void* v,
+                                        void* q_out, void* k_cache, void* v_cache,
+                                        const void* cos, const void* sin,
+                                        const void* q_w, const void* k_w, float eps,
+                                        int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+                                        int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                                        int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                                        int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                                        int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                                        int64_t c_sb, int64_t c_sh, int64_t c_ss,
+                                        int64_t capacity, int64_t pos, const int64_t* pos_dev,
+                                        int64_t cs_sb, int64_t cs_ss, void* stream);
+
 /* Epilogue activations for umic_linear_bf16. */
 #define UMIC_ACT_NONE 0
 #define UMIC_ACT_GELU 1      /* exact erf GELU */

@@ -36,7 +36,8 @@ def test_header_declares_expected_entry_points():
     for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
               "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
               "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
-              "umic_rope_kv_append_bf16", "umic_version", "umic_error_string"):
+              "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
+              "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -129,6 +130,39 @@ def test_argument_rejection_before_launch(lib):
     assert ok(4, 128, -1, 0) == E_ARG             # negative capacity
     assert ok(4, 128, 16, 0, ptrs=[fake] * 5 + [None] + [fake] * 2) == E_ARG  # no v cache
     assert ok(0, 128, 16, 0, ptrs=[None] * 8) == 0   # empty: nothing launched
+
+
+def test_qk_norm_rope_rejection(lib):
+    """Argument checks of the fused q/k RMSNorm + RoPE entry points, before
+    any launch (no GPU needed): bad sizes, head dims the row group cannot
+    take, missing weights, misalignment; empty inputs are no-ops."""
+    E_ARG, E_UNS = -1, -2
+    f = lib.umic_qk_rmsnorm_rope_bf16
+    fake = 1 << 20   # 16-byte aligned, never dereferenced: every case returns early
+    strides = [1024, 1024, 128] * 4
+    assert f(None, None, None, None, None, None, 1e-6, None, None, 1, 0, 4, 1, 128,
+             *strides, 128, 128, None) == 0                             # S = 0: no-op
+    assert f(fake, fake, fake, fake, fake, fake, 1e-6, fake, fake, -1, 4, 4, 1, 128,
+             *strides, 128, 128, None) == E_ARG
+    assert f(fake, fake, fake, fake, fake, fake, 1e-6, fake, fake, 1, 4, 4, 1, 96,
+             *strides, 128, 128, None) == E_UNS                         # 96/16 = 6
+    assert f(fake, fake, fake, fake, fake, fake, 1e-6, fake, fake, 1, 4, 4, 1, 136,
+             *strides, 128, 128, None) == E_UNS                         # 136 % 16
+    assert f(fake, fake, fake, fake, None, fake, 1e-6, fake, fake, 1, 4, 4, 1, 128,
+             *strides, 128, 128, None) == E_ARG                         # no q weight
+    assert f(fake + 2, fake, fake, fake, fake, fake, 1e-6, fake, fake, 1, 4, 4, 1, 128,
+             *strides, 128, 128, None) == E_UNS                         # misaligned q
+    g = lib.umic_qk_rmsnorm_rope_kv_append_bf16
+    kv = [1024, 1024, 128] * 4 + [4096, 4096, 128]
+    assert g(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1e-6, 1, 4, 4, 1, 128,
+             *kv[:12], 8 * 4096 * 128, 4096 * 128, 128, 100, 98, None, 128, 128,
+             None) == E_ARG                                             # 98 + 4 > 100
+    assert g(fake, fake, fake, fake, fake, fake, fake, fake, fake, None, 1e-6, 1, 4, 4, 1, 128,
+             *kv[:12], 8 * 4096 * 128, 4096 * 128, 128, 100, 0, None, 128, 128,
+             None) == E_ARG                                             # no k weight
+    assert g(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1e-6, 1, 4, 4, 1, 80,
+             *kv[:12], 8 * 4096 * 80, 4096 * 80, 80, 100, 0, None, 80, 80,
+             None) == E_UNS                                             # 80/16 = 5
 
 
 def test_wrappers_refuse_cpu_tensors():

@@ -102,13 +102,16 @@ def test_decode_graph_runner_matches_eager(monkeypatch):
     # with no graphs yet, the first two steps are eager warm-up
     assert captured == [NEW - 3, NEW - 1, NEW - 1, NEW - 3]
     assert runner.replays == (NEW - 3) + (NEW - 1) + (NEW - 1) + (NEW - 3)
-    assert log["umic_rope_kv_append_bf16"] > 0      # the fused append ran in the graphs
+    # q/k norms, RoPE and the append ran fused in the graphs, norms and RoPE
+    # fused at prefill
+    assert log["umic_qk_rmsnorm_rope_kv_append_bf16"] > 0
+    assert log["umic_qk_rmsnorm_rope_bf16"] > 0
 
 
 def test_flow_step_graph_replays_match_eager():
     """FlowStepGraph over a flow-expert-like step: 32 action tokens through a
-    config-5 decoder layer that appends to an in-place KV cache (RoPE and the
-    append fused) and attends to the whole prefix, then crops back.  Ten
+    config-5 decoder layer that appends to an in-place KV cache (q/k norms,
+    RoPE and the append fused) and attends to the whole prefix, then crops back.  Ten
     steps with new x and t: each replay equals the eager step bit for bit,
     and the cache prefix is untouched."""
     from torch.nn.attention import SDPBackend, sdpa_kernel

@@ -19,7 +19,7 @@ import collections
 import numpy as np
 import pytest
 import torch
-from helpers import bf16_randn, bits, max_rel_err, qwen3_decoder_layer, rel_err
+from helpers import bf16_randn, bits, max_rel_err, qwen3_decoder_layer, rel_err, ulp
 
 import oracle
 from umic import _lib, integrate
@@ -218,9 +218,9 @@ def test_decoder_layer_flow_step_on_the_inplace_cache(call_log):
     """BASELINE config 5 decoder layer: prefill 3094 tokens into a
     DynamicCache, then append a 32-token flow step that attends to the whole
     prefix and to itself (non-causal, no mask) -- eager on the DynamicCache
-    vs fuse_kv_rope on an InplaceKVCache.  The cache rows must be
-    bit-identical (same projections, the kernel's rotation is the eager
-    chain's) and the layer output equal within the GEMM tolerance (the
+    vs fuse_kv_rope on an InplaceKVCache (q/k norms, RoPE and append in one
+    launch).  The new cache rows must be the oracle's (from the layer's own
+    k projection) and the layer output equal within the GEMM tolerance (the
     attention reads strided cache views instead of contiguous tensors).
     Attention is held to the flash / memory-efficient SDPA kernels: an
     unsupported case raises rather than running the bf16 math path."""
@@ -242,13 +242,23 @@ def test_decoder_layer_flow_step_on_the_inplace_cache(call_log):
         ref = layer(x, position_embeddings=cs, past_key_values=dyn, is_causal=False)
         assert integrate.fuse_kv_rope(layer) == 1
         out = layer(x, position_embeddings=cs, past_key_values=conv, is_causal=False)
+        k_raw = layer.self_attn.k_proj(layer.input_layernorm(x)).view(1, N, -1, 128)
         torch.cuda.synchronize()
     integrate.unfuse_mlps(layer)
-    assert call_log["umic_rope_kv_append_bf16"] == 1
+    # q_norm, k_norm, RoPE and the append: one launch
+    assert call_log["umic_qk_rmsnorm_rope_kv_append_bf16"] == 1
+    assert call_log["umic_rope_kv_append_bf16"] == 0
     lyr = conv.layers[0]
     assert lyr.get_seq_length() == P + N
-    assert torch.equal(lyr.keys, dyn.layers[0].keys) and torch.equal(lyr.values,
-                                                                     dyn.layers[0].values)
+    assert torch.equal(lyr.values, dyn.layers[0].values)
+    assert torch.equal(lyr.keys[:, :, :P], dyn.layers[0].keys[:, :, :P])
+    # the new rows are the oracle's; eager's fp32 norm statistic may round
+    # across a boundary the exact one does not, one bf16 ulp at most
+    kn = oracle.rmsnorm(bits(k_raw), bits(layer.self_attn.k_norm.weight),
+                        layer.self_attn.k_norm.variance_epsilon)
+    krot = oracle.rope_text(kn[0], bits(cs[0])[0], bits(cs[1])[0])
+    assert np.array_equal(bits(lyr.keys[:, :, P:])[0], krot.transpose(1, 0, 2))
+    assert ulp(bits(lyr.keys), bits(dyn.layers[0].keys)).max() <= 1
     e1, e2 = max_rel_err(out, ref), rel_err(out, ref)
     print(f"flow step on the in-place cache: max_rel {e1:.2e} rel {e2:.2e}", flush=True)
     assert e1 <= 2e-2 and e2 <= 2e-2

@@ -46,6 +46,10 @@ struct RopeArgs {
   // launch-uniform divisors of the item decomposition: items per position,
   // chunks per half row, head dim (set per launch; see SmallDiv)
   SmallDiv ipp, chunks, dim;
+  // RMSNorm of q / k head rows before the rotation (norm kernels only)
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
 };
 
 // Items per position are bounded (checked on the host) so that every
@@ -224,7 +228,35 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
 // bf16 tables, 16-byte chunks: cos/sin read per item from global (see the
 // header).  kDirectItems items per thread, all q/k loads issued first.
 constexpr int kDirectItems = 2;
-template <int MODE>
+
+// RMSNorm of a head row ahead of its rotation: the text attention's q_norm /
+// k_norm, HF Qwen3VLTextRMSNorm, bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).
+// A head row is G = D/16 items, one per lane, on G consecutive lanes that
+// start at a multiple of G (rows start at multiples of G items and a block's
+// items are lane-ordered); each lane holds chunk c of both halves.  The sum
+// of squares is exact in double for bf16 data, so the butterfly order does
+// not change it: every lane of the row gets the row's statistics as a serial
+// sum would, the mean is rounded once to fp32 and the reciprocal square root
+// is correctly rounded -- the norm kernel's numerics.  Called with the whole
+// row active (rows are skipped or kept as a unit).
+__device__ __forceinline__ void rms_norm_chunks(float (&xl)[8], float (&xh)[8],
+                                                const uint16_t* w, int dl, int half, int G,
+                                                double inv_d, float eps) {
+  double ss = 0.0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += (double)(xl[e] * xl[e]) + (double)(xh[e] * xh[e]);
+  for (int m = 1; m < G; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+  const float rstd = rsqrt_cr((float)(ss * inv_d) + eps);
+  float wl[8], wh[8];
+  unpack8(*reinterpret_cast<const u32x4*>(w + dl), wl);
+  unpack8(*reinterpret_cast<const u32x4*>(w + half + dl), wh);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xl[e] = rbf(wl[e] * rbf(xl[e] * rstd));
+    xh[e] = rbf(wh[e] * rbf(xh[e] * rstd));
+  }
+}
+template <int MODE, bool NORM = false>
 __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   constexpr int VEC = 8;
   const int64_t npos = a.B * a.S;
@@ -241,7 +273,7 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   uint16_t* os[kDirectItems];
   int64_t cso[kDirectItems];
   int dls[kDirectItems];
-  bool ok[kDirectItems];
+  bool ok[kDirectItems], qrow[kDirectItems];
 #pragma unroll
   for (int u = 0; u < kDirectItems; ++u) {
     const int l = u * 256 + (int)threadIdx.x;
@@ -256,6 +288,7 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
       sidx = p - b * a.S;
     }
     const bool isq = j < nq;
+    qrow[u] = isq;
     const int jj = isq ? j : j - nq;
     int c;
     const int h = div_small(a.chunks, jj, c);
@@ -278,6 +311,9 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
 #pragma unroll
   for (int u = 0; u < kDirectItems; ++u) {
     if (!ok[u]) continue;
+    if constexpr (NORM)
+      rms_norm_chunks(xl[u], xh[u], qrow[u] ? a.qw : a.kw, dls[u], half, a.chunks.d,
+                      1.0 / (double)D, a.eps);
     float cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
     load_cs8<false>(a.cos, cso[u] + dls[u], cl);
     load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
@@ -312,8 +348,12 @@ struct KvArgs {
   int64_t c_sb, c_sh, c_ss, cap, pos;
   int64_t cs_sb, cs_ss;
   SmallDiv ipp, chunks;  // items per position, chunks per half row
+  const uint16_t* qw;    // RMSNorm of q / k head rows (norm kernel only)
+  const uint16_t* kw;
+  float eps;
 };
 
+template <bool NORM = false>
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
   constexpr int VEC = 8;
   const int half = (int)a.D / 2;
@@ -385,6 +425,9 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
     float xl[VEC], xh[VEC], cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
     unpack8(rl[u], xl);
     unpack8(rh[u], xh);
+    if constexpr (NORM)
+      rms_norm_chunks(xl, xh, kind[u] == 0 ? a.qw : a.kw, dls[u], half, a.chunks.d,
+                      1.0 / (double)a.D, a.eps);
     load_cs8<false>(a.cos, cso[u] + dls[u], cl);
     load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
     load_cs8<false>(a.sin, cso[u] + dls[u], sl);
@@ -503,13 +546,26 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   return dispatch_vec<UMIC_ROPE_VISION, false>(a, vec, direct_ok, st);
 }
 
-extern "C" int umic_rope_kv_append_bf16(
-    const void* q, const void* k, const void* v, void* q_out, void* k_cache, void* v_cache,
-    const void* cos, const void* sin, int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
-    int64_t q_sb, int64_t q_ss, int64_t q_sh, int64_t k_sb, int64_t k_ss, int64_t k_sh,
-    int64_t v_sb, int64_t v_ss, int64_t v_sh, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
-    int64_t c_sb, int64_t c_sh, int64_t c_ss, int64_t capacity, int64_t pos,
-    const int64_t* pos_dev, int64_t cs_sb, int64_t cs_ss, void* stream) {
+namespace umic {
+namespace {
+
+// head_dim values the fused RMSNorm takes: 16-byte chunks (D % 16 == 0) and
+// a row group of D/16 lanes that is a power of two within one wavefront.
+bool norm_dim_ok(int64_t D) {
+  const int64_t g = D / 16;
+  return D % 16 == 0 && g >= 1 && g <= kWave && (g & (g - 1)) == 0;
+}
+
+// The in-place cache append, optionally with the q / k RMSNorm (qw, kw
+// non-null).  Shared by umic_rope_kv_append_bf16 and its norm variant.
+int kv_append_impl(const void* q, const void* k, const void* v, void* q_out, void* k_cache,
+                   void* v_cache, const void* cos, const void* sin, const void* qw,
+                   const void* kw, float eps, bool norm, int64_t B, int64_t S, int64_t Hq,
+                   int64_t Hk, int64_t D, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                   int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t v_sb, int64_t v_ss,
+                   int64_t v_sh, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh, int64_t c_sb,
+                   int64_t c_sh, int64_t c_ss, int64_t capacity, int64_t pos,
+                   const int64_t* pos_dev, int64_t cs_sb, int64_t cs_ss, void* stream) {
   if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0 || capacity < 0) return UMIC_ERR_INVALID_ARG;
   // a known write position must fit the cache (the reference raises on overflow)
   if (!pos_dev && (pos < 0 || pos + S > capacity)) return UMIC_ERR_INVALID_ARG;
@@ -519,12 +575,18 @@ extern "C" int umic_rope_kv_append_bf16(
   if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
   if (Hq > 0 && (!q || !q_out)) return UMIC_ERR_INVALID_ARG;
   if (Hk > 0 && (!k || !v || !k_cache || !v_cache)) return UMIC_ERR_INVALID_ARG;
+  if (norm) {
+    if ((Hq > 0 && !qw) || (Hk > 0 && !kw)) return UMIC_ERR_INVALID_ARG;
+    if (!norm_dim_ok(D) || (qw && (uintptr_t)qw % 16) || (kw && (uintptr_t)kw % 16))
+      return UMIC_ERR_UNSUPPORTED;
+  }
 
   KvArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)q_out,
            (uint16_t*)k_cache, (uint16_t*)v_cache, (const uint16_t*)cos, (const uint16_t*)sin,
            pos_dev, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh,
            qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss,
-           small_div((int)((Hq + 2 * Hk) * (D / 16))), small_div((int)(D / 16))};
+           small_div((int)((Hq + 2 * Hk) * (D / 16))), small_div((int)(D / 16)),
+           (const uint16_t*)qw, (const uint16_t*)kw, eps};
   bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
             (uintptr_t)sin % 16 == 0;
   if (Hq) {
@@ -546,7 +608,87 @@ extern "C" int umic_rope_kv_append_bf16(
   const int64_t nitems = B * S * (Hq + 2 * Hk) * (D / 16);
   const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     as_stream(stream), a);
+  if (norm)
+    hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
+                       as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(rope_kv_append_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+                       as_stream(stream), a);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace umic
+
+extern "C" int umic_rope_kv_append_bf16(
+    const void* q, const void* k, const void* v, void* q_out, void* k_cache, void* v_cache,
+    const void* cos, const void* sin, int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+    int64_t q_sb, int64_t q_ss, int64_t q_sh, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+    int64_t v_sb, int64_t v_ss, int64_t v_sh, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+    int64_t c_sb, int64_t c_sh, int64_t c_ss, int64_t capacity, int64_t pos,
+    const int64_t* pos_dev, int64_t cs_sb, int64_t cs_ss, void* stream) {
+  return kv_append_impl(q, k, v, q_out, k_cache, v_cache, cos, sin, nullptr, nullptr, 0.f,
+                        false, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss,
+                        v_sh, qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, pos_dev,
+                        cs_sb, cs_ss, stream);
+}
+
+extern "C" int umic_qk_rmsnorm_rope_kv_append_bf16(
+    const void* q, const void* k, const void* v, void* q_out, void* k_cache, void* v_cache,
+    const void* cos, const void* sin, const void* q_w, const void* k_w, float eps, int64_t B,
+    int64_t S, int64_t Hq, int64_t Hk, int64_t D, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    int64_t k_sb, int64_t k_ss, int64_t k_sh, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    int64_t qo_sb, int64_t qo_ss, int64_t qo_sh, int64_t c_sb, int64_t c_sh, int64_t c_ss,
+    int64_t capacity, int64_t pos, const int64_t* pos_dev, int64_t cs_sb, int64_t cs_ss,
+    void* stream) {
+  return kv_append_impl(q, k, v, q_out, k_cache, v_cache, cos, sin, q_w, k_w, eps, true, B, S,
+                        Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh, qo_sb,
+                        qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, pos_dev, cs_sb, cs_ss,
+                        stream);
+}
+
+extern "C" int umic_qk_rmsnorm_rope_bf16(const void* q, const void* k, void* q_out, void* k_out,
+                                        const void* q_w, const void* k_w, float eps,
+                                        const void* cos, const void* sin, int64_t B, int64_t S,
+                                        int64_t Hq, int64_t Hk, int64_t D, int64_t q_sb,
+                                        int64_t q_ss, int64_t q_sh, int64_t k_sb, int64_t k_ss,
+                                        int64_t k_sh, int64_t qo_sb, int64_t qo_ss,
+                                        int64_t qo_sh, int64_t ko_sb, int64_t ko_ss,
+                                        int64_t ko_sh, int64_t cs_sb, int64_t cs_ss,
+                                        void* stream) {
+  if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
+  if (!norm_dim_ok(D)) return UMIC_ERR_UNSUPPORTED;
+  if ((Hq + Hk) * (D / 2) >= kMaxItemsPerPos) return UMIC_ERR_UNSUPPORTED;
+  if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;  // empty: pointers may be null
+  if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
+  if (Hq > 0 && (!q || !q_out || !q_w)) return UMIC_ERR_INVALID_ARG;
+  if (Hk > 0 && (!k || !k_out || !k_w)) return UMIC_ERR_INVALID_ARG;
+  // the direct text kernel only: 16-byte chunks everywhere
+  bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
+            (uintptr_t)sin % 16 == 0;
+  if (Hq)
+    ok = ok && q_sb % 8 == 0 && q_ss % 8 == 0 && q_sh % 8 == 0 && qo_sb % 8 == 0 &&
+         qo_ss % 8 == 0 && qo_sh % 8 == 0 && (uintptr_t)q % 16 == 0 &&
+         (uintptr_t)q_out % 16 == 0 && (uintptr_t)q_w % 16 == 0;
+  if (Hk)
+    ok = ok && k_sb % 8 == 0 && k_ss % 8 == 0 && k_sh % 8 == 0 && ko_sb % 8 == 0 &&
+         ko_ss % 8 == 0 && ko_sh % 8 == 0 && (uintptr_t)k % 16 == 0 &&
+         (uintptr_t)k_out % 16 == 0 && (uintptr_t)k_w % 16 == 0;
+  if (!ok) return UMIC_ERR_UNSUPPORTED;
+  RopeArgs a{(const uint16_t*)q, (const uint16_t*)k, (uint16_t*)q_out, (uint16_t*)k_out,
+             cos, sin, B, S, Hq, Hk, D,
+             q_sb, q_ss, q_sh, k_sb, k_ss, k_sh,
+             qo_sb, qo_ss, qo_sh, ko_sb, ko_ss, ko_sh, cs_sb, cs_ss};
+  if (Hq == 0) a.q = a.qo = nullptr;
+  if (Hk == 0) a.k = a.ko = nullptr;
+  a = with_divisors<8>(a);
+  a.qw = (const uint16_t*)q_w;
+  a.kw = (const uint16_t*)k_w;
+  a.eps = eps;
+  const int64_t nitems = B * S * (Hq + Hk) * (D / 16);
+  const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((rope_qk_direct_kernel<UMIC_ROPE_TEXT, true>), dim3((unsigned)blocks),
+                     dim3(256), 0, as_stream(stream), a);
   return launch_status();
 }

@@ -102,30 +102,35 @@ class InplaceLayer(DynamicLayer):
         self._v_buf[:, :, self._pos:self._pos + n, :] = value_states
         return self._advance(n)
 
-    def can_append_rotary(self, q, k, v, cos, sin) -> bool:
+    def can_append_rotary(self, q, k, v, cos, sin, norm=None) -> bool:
         """True when ``append_rotary`` takes its one-launch fused path."""
-        return self._fused_ok and rope.kv_inputs_ok(q, k, v, cos, sin, self._k_buf)
+        return (self._fused_ok and rope.kv_inputs_ok(q, k, v, cos, sin, self._k_buf)
+                and (norm is None or rope.norm_weights_ok(q, norm[0], norm[1])))
 
     def append_rotary(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                      cos: torch.Tensor, sin: torch.Tensor):
+                      cos: torch.Tensor, sin: torch.Tensor, norm=None):
         """rope(q), and the cache after appending rope(k) and v, in one launch.
 
         Equivalent to ``apply_rotary_pos_emb(q, k, cos, sin)`` followed by
         ``update(k_rot, v)`` (bit for bit: the kernel's rotation is the eager
         bf16 chain's); returns ``(q_rot, keys, values)`` with ``update``'s
         return conventions, or None -- nothing done -- when the inputs are not
-        a layout the kernel takes (``can_append_rotary``).
+        a layout the kernel takes (``can_append_rotary``).  With
+        ``norm = (q_w, k_w, eps)``, q and k are the raw projections and the
+        attention's per-head RMSNorms (HF q_norm / k_norm) run first, in the
+        same launch.
         """
-        if not self.can_append_rotary(q, k, v, cos, sin):
+        if not self.can_append_rotary(q, k, v, cos, sin, norm):
             return None
         n = k.shape[2]
         if self._graph_write(n):
             if not (self._pos_t.dtype == torch.int64 and self._pos_t.device == self.device):
                 return None
-            q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, 0, self._pos_t)
+            q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, 0, self._pos_t,
+                                   norm)
             return (q_rot, *self._graph_views())
         self._check_room(n)
-        q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, self._pos, None)
+        q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, self._pos, None, norm)
         return (q_rot, *self._advance(n))
 
     def get_seq_length(self, cache_position=None) -> int:

@@ -623,38 +623,79 @@ def _attention_interface(module: nn.Module):
     return ALL_ATTENTION_FUNCTIONS.get_interface(impl, eager)
 
 
+def _head_norms(module: nn.Module, q: torch.Tensor):
+    """``(q_w, k_w, eps)`` when the attention's q_norm / k_norm are RMSNorms
+    (class name contains "rmsnorm", 1-D weight, one eps) that the fused
+    norm + RoPE kernels take for ``q``; else None."""
+    qn, kn = getattr(module, "q_norm", None), getattr(module, "k_norm", None)
+    if not all("rmsnorm" in type(n).__name__.lower() for n in (qn, kn)):
+        return None
+    qw, kw = getattr(qn, "weight", None), getattr(kn, "weight", None)
+    eps = _norm_eps(qn)
+    if eps != _norm_eps(kn) or not rope.norm_weights_ok(q, qw, kw):
+        return None
+    return qw, kw, eps
+
+
 def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
                                      attention_mask=None, past_key_values=None, **kwargs):
-    """Text attention whose RoPE and KV-cache append are one kernel launch.
+    """Text attention whose q/k norms, RoPE and KV-cache append are one launch.
 
-    Taken when the cache is an ``InplaceKVCache`` and the layouts are ones
-    the kernel handles; the projections, q/k norms, attention and output
-    projection are the module's own (same order and arguments as the
-    transformers forward).  Anything else runs the class forward unchanged.
+    The projections, attention and output projection are the module's own
+    (same order and arguments as the transformers forward, modeling_qwen3_vl
+    ``Qwen3VLTextAttention.forward``).  Between them:
+
+    * cache an ``InplaceKVCache``: q_norm, k_norm, RoPE and the append in one
+      launch (``umic_qk_rmsnorm_rope_kv_append_bf16``), or RoPE and the
+      append when the norms are not RMSNorms the kernel takes;
+    * any other cache, or none: q_norm, k_norm and RoPE in one launch
+      (``umic_qk_rmsnorm_rope_bf16``), then the cache's own ``update``;
+    * otherwise the module's norms, ``apply_rotary_pos_emb`` and ``update``.
+
+    Training, or autograd through any weight or the input, runs the class
+    forward.
     """
     from umic.cache import InplaceKVCache, InplaceLayer
 
+    if self.training or grad_needed(hidden_states, self.q_proj.weight, self.k_proj.weight,
+                                    self.v_proj.weight, getattr(self.q_norm, "weight", None),
+                                    getattr(self.k_norm, "weight", None)):
+        return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
+                                  past_key_values=past_key_values, **kwargs)
     layer = None
     if isinstance(past_key_values, InplaceKVCache) and self.layer_idx < len(
             past_key_values.layers):
         layer = past_key_values.layers[self.layer_idx]
-    if (not isinstance(layer, InplaceLayer) or self.training
-            or grad_needed(hidden_states, self.q_proj.weight, self.k_proj.weight,
-                           self.v_proj.weight)):
-        return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
-                                  past_key_values=past_key_values, **kwargs)
+        if not isinstance(layer, InplaceLayer):
+            layer = None
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    q = self.q_norm(self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
-    k = self.k_norm(self.k_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+    q_raw = self.q_proj(hidden_states).view(hidden_shape)
+    k_raw = self.k_proj(hidden_states).view(hidden_shape)
     v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
     cos, sin = position_embeddings
-    fused = layer.append_rotary(q, k, v, cos, sin)
+    q, k = q_raw.transpose(1, 2), k_raw.transpose(1, 2)
+    norm = _head_norms(self, q)
+    fused = None
+    if norm is not None:
+        if layer is not None:
+            fused = layer.append_rotary(q, k, v, cos, sin, norm)
+        elif rope.qk_norm_rope_eligible(q, k, cos, sin, norm[0], norm[1]):
+            q, k = rope.qk_norm_rope(q, k, cos, sin, *norm)
+            if past_key_values is not None:
+                k, v = past_key_values.update(k, v, self.layer_idx)
+            fused = (q, k, v)
+    if fused is None:
+        q = self.q_norm(q_raw).transpose(1, 2)
+        k = self.k_norm(k_raw).transpose(1, 2)
+        if layer is not None:
+            fused = layer.append_rotary(q, k, v, cos, sin)
     if fused is not None:
         q, k, v = fused
     else:
         q, k = _qwen3_vl_module().apply_rotary_pos_emb(q, k, cos, sin)
-        k, v = past_key_values.update(k, v, self.layer_idx)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx)
     attn = _attention_interface(self)
     out, weights = attn(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling,
                         **kwargs)
@@ -663,11 +704,13 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
 
 
 def fuse_kv_rope(model: nn.Module, dry_run: bool = False) -> int:
-    """Route text attention through the fused RoPE + in-place cache append.
+    """Route text attention through the fused q/k norms + RoPE (+ append).
 
-    Only calls whose ``past_key_values`` is an ``InplaceKVCache`` change
-    path (see ``fuse_repeat_cache``); with any other cache, or none, the
-    patched forward is the class forward.
+    With an ``InplaceKVCache`` (see ``fuse_repeat_cache``) the per-head
+    q_norm / k_norm, the RoPE and the cache append are one launch; with any
+    other cache, or none, the norms and the RoPE are one launch followed by
+    the cache's own ``update``.  Layouts or norms the kernels do not take
+    run the module's own steps.
 
     Returns:
         Number of attention modules matched (and patched unless dry_run).

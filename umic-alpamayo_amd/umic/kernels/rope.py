@@ -228,23 +228,76 @@ def kv_append_eligible(q, k, v, cos, sin, k_cache, v_cache) -> bool:
 
 
 def kv_launch(q, k, v, cos, sin, k_cache, v_cache, pos: int,
-              pos_t: torch.Tensor | None) -> torch.Tensor:
-    """Launch umic_rope_kv_append_bf16 on inputs already checked by
-    ``kv_append_eligible``; returns rope(q).  The C entry point re-validates
-    strides, alignment and (without pos_t) the write range before launching."""
+              pos_t: torch.Tensor | None, norm=None) -> torch.Tensor:
+    """Launch umic_rope_kv_append_bf16 (or, with ``norm = (q_w, k_w, eps)``,
+    umic_qk_rmsnorm_rope_kv_append_bf16: q_norm / k_norm applied first) on
+    inputs already checked by ``kv_append_eligible`` (and ``norm_weights_ok``);
+    returns rope(q).  The C entry point re-validates strides, alignment and
+    (without pos_t) the write range before launching."""
     B, Hq, S, D = q.shape
     q_out = torch.empty_like(q)
     qs, ks, vs, os_, cst = q.stride(), k.stride(), v.stride(), q_out.stride(), k_cache.stride()
+    head = (q.data_ptr(), k.data_ptr(), v.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(),
+            v_cache.data_ptr(), cos.data_ptr(), sin.data_ptr())
+    if norm is not None:
+        name, head = ("umic_qk_rmsnorm_rope_kv_append_bf16",
+                      head + (norm[0].data_ptr(), norm[1].data_ptr(), float(norm[2])))
+    else:
+        name = "umic_rope_kv_append_bf16"
     with _lib.device_of(q):
-        _lib.call("umic_rope_kv_append_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                  q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos.data_ptr(),
-                  sin.data_ptr(), B, S, Hq, k.shape[1], D,
+        _lib.call(name, *head, B, S, Hq, k.shape[1], D,
                   qs[0], qs[2], qs[1], ks[0], ks[2], ks[1], vs[0], vs[2], vs[1],
                   os_[0], os_[2], os_[1], cst[0], cst[1], cst[2], k_cache.shape[2], pos,
                   None if pos_t is None else pos_t.data_ptr(),
                   cos.stride(0) if cos.shape[0] == B else 0, cos.stride(1),
                   _lib.stream_of(q))
     return q_out
+
+
+def norm_weights_ok(q, q_w, k_w) -> bool:
+    """Head-row RMSNorm weights the fused norm + RoPE kernels take: [D] bf16,
+    contiguous, 16-byte aligned, on q's device, with D/16 a power of two up to
+    64 (one row per aligned group of D/16 lanes)."""
+    D = q.shape[-1]
+    g = D // 16
+    if D % 16 or not 1 <= g <= 64 or g & (g - 1):
+        return False
+    return all(isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16 and w.dim() == 1
+               and w.shape[0] == D and w.is_contiguous() and w.device == q.device
+               and w.data_ptr() % 16 == 0 for w in (q_w, k_w))
+
+
+def qk_norm_rope_eligible(q, k, cos, sin, q_w, k_w) -> bool:
+    """The HF text layout of ``text_rope_eligible`` with 16-byte chunks
+    everywhere, plus norm weights the fused kernel takes."""
+    return (text_rope_eligible(q, k, cos, sin) and norm_weights_ok(q, q_w, k_w)
+            and _vec_ok(q, k, cos, sin))
+
+
+def qk_norm_rope(q, k, cos, sin, q_w, k_w, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The text attention's q_norm / k_norm on every head row, then HF
+    apply_rotary_pos_emb, in one launch (umic_qk_rmsnorm_rope_bf16).
+
+    q [B,Hq,S,D] and k [B,Hk,S,D] are the projections as HF views them
+    (``proj(x).view(B,S,H,D).transpose(1,2)``) BEFORE the norms -- a head-row
+    norm commutes with that transpose; q_w, k_w are the norms' [D] weights.
+    Returns (q_embed, k_embed) allocated like eager's (``torch.empty_like``).
+    Bit-identical to rmsnorm_hip on each head row followed by the text RoPE.
+    """
+    require_device(q, k, cos, sin, q_w, k_w)
+    if not qk_norm_rope_eligible(q, k, cos, sin, q_w, k_w):
+        raise ValueError(f"qk_norm_rope: unsupported layout q{tuple(q.shape)} k{tuple(k.shape)}")
+    B, Hq, S, D = q.shape
+    Hk = k.shape[1]
+    q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+    qs, ks = _strides_bsh(q, "bhsd"), _strides_bsh(k, "bhsd")
+    qos, kos = _strides_bsh(q_out, "bhsd"), _strides_bsh(k_out, "bhsd")
+    with _lib.device_of(q):
+        _lib.call("umic_qk_rmsnorm_rope_bf16", q.data_ptr(), k.data_ptr(), q_out.data_ptr(),
+                  k_out.data_ptr(), q_w.data_ptr(), k_w.data_ptr(), float(eps),
+                  cos.data_ptr(), sin.data_ptr(), B, S, Hq, Hk, D, *qs, *ks, *qos, *kos,
+                  cos.stride(0) if cos.shape[0] == B else 0, cos.stride(1), _lib.stream_of(q))
+    return q_out, k_out
 
 
 def rope_kv_append(q, k, v, cos, sin, k_cache, v_cache, pos: int,
