@@ -50,6 +50,7 @@ struct RopeArgs {
   const uint16_t* qw;
   const uint16_t* kw;
   float eps;
+  double inv_d;          // 1 / D
 };
 
 // Items per position are bounded (checked on the host) so that every
@@ -226,8 +227,17 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
 }
 
 // bf16 tables, 16-byte chunks: cos/sin read per item from global (see the
-// header).  kDirectItems items per thread, all q/k loads issued first.
-constexpr int kDirectItems = 2;
+// header).  IT items per thread, all q/k loads issued first.  With one
+// item a thread also issues its cos/sin (and norm weight) loads before any
+// arithmetic, so a wave waits for memory once; with two, holding both items'
+// tables costs occupancy (84 against 70 VGPRs) and the tables are loaded per
+// item instead.  Measured at q[1,32,3100,128] + k[1,8,...]: plain RoPE 14.5 us
+// with two items (14.9 with one), the norm variant 19.7 us with one (21.3
+// with two), the KV append 15.5 / 20.5 us (plain / norm) with one (17.1 /
+// 22.5 with two).
+template <bool NORM>
+constexpr int direct_items() { return NORM ? 1 : 2; }
+constexpr int kKvItems = 1;
 
 // RMSNorm of a head row ahead of its rotation: the text attention's q_norm /
 // k_norm, HF Qwen3VLTextRMSNorm, bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).
@@ -239,26 +249,74 @@ constexpr int kDirectItems = 2;
 // sum would, the mean is rounded once to fp32 and the reciprocal square root
 // is correctly rounded -- the norm kernel's numerics.  Called with the whole
 // row active (rows are skipped or kept as a unit).
+// v from another lane of the same 16-lane row (DPP control CTRL), both
+// 32-bit halves moved with v_mov_dpp.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
 __device__ __forceinline__ void rms_norm_chunks(float (&xl)[8], float (&xh)[8],
-                                                const uint16_t* w, int dl, int half, int G,
-                                                double inv_d, float eps) {
-  double ss = 0.0;
+                                                const u32x4 (&w)[2], int G, double inv_d,
+                                                float eps) {
+  // four partial sums: shorter dependency chains, same exact total
+  double s4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss += (double)(xl[e] * xl[e]) + (double)(xh[e] * xh[e]);
-  for (int m = 1; m < G; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+  for (int e = 0; e < 8; ++e) s4[e & 3] += (double)(xl[e] * xl[e]) + (double)(xh[e] * xh[e]);
+  double ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  // butterfly within the row's G lanes: DPP moves inside a 16-lane row (full
+  // rate, no LDS crossbar), then shuffles for G = 32, 64.  After the quad
+  // steps every lane of a quad holds the quad sum, so the half-row and row
+  // mirrors add the partner quad / half.  G is launch-uniform.
+  if (G >= 2) ss += dpp_move<0xB1>(ss);   // quad_perm [1,0,3,2]: lane ^ 1
+  if (G >= 4) ss += dpp_move<0x4E>(ss);   // quad_perm [2,3,0,1]: lane ^ 2
+  if (G >= 8) ss += dpp_move<0x141>(ss);  // row_half_mirror: lane ^ 7 in 8
+  if (G >= 16) ss += dpp_move<0x140>(ss); // row_mirror: lane ^ 15 in 16
+  for (int m = 16; m < G; m <<= 1) ss += __shfl_xor(ss, m, kWave);
   const float rstd = rsqrt_cr((float)(ss * inv_d) + eps);
   float wl[8], wh[8];
-  unpack8(*reinterpret_cast<const u32x4*>(w + dl), wl);
-  unpack8(*reinterpret_cast<const u32x4*>(w + half + dl), wh);
+  unpack8(w[0], wl);
+  unpack8(w[1], wh);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     xl[e] = rbf(wl[e] * rbf(xl[e] * rstd));
     xh[e] = rbf(wh[e] * rbf(xh[e] * rstd));
   }
 }
+
+// One 16-byte bf16 chunk at element offset off of base.
+__device__ __forceinline__ u32x4 ld_chunk(const void* base, int64_t off) {
+  return *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off);
+}
+
+// The cos/sin chunks of an item (low and high half of each table) and, for
+// the norm kernels, its row's weight chunks -- all loads of a thread are
+// issued before any item is computed, so a wave waits for memory once.
+struct ItemTables {
+  u32x4 cs[4];  // cos lo, cos hi, sin lo, sin hi
+  u32x4 w[2];   // norm weight lo, hi
+};
+
+template <bool NORM>
+__device__ __forceinline__ void load_item_tables(ItemTables& t, const void* cos, const void* sin,
+                                                 int64_t cso, int dl, int half,
+                                                 const uint16_t* w) {
+  t.cs[0] = ld_chunk(cos, cso + dl);
+  t.cs[1] = ld_chunk(cos, cso + half + dl);
+  t.cs[2] = ld_chunk(sin, cso + dl);
+  t.cs[3] = ld_chunk(sin, cso + half + dl);
+  if constexpr (NORM) {
+    t.w[0] = ld_chunk(w, dl);
+    t.w[1] = ld_chunk(w, half + dl);
+  }
+}
+
 template <int MODE, bool NORM = false>
 __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   constexpr int VEC = 8;
+  constexpr int IT = direct_items<NORM>();
   const int64_t npos = a.B * a.S;
   const int D = (int)a.D;
   const int half = D / 2;
@@ -266,16 +324,16 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
   const int nq = (int)a.Hq * a.chunks.d;
   const int64_t nitems = npos * ipp;
   // block-level decomposition once, per item small divisions (SmallDiv)
-  const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const int64_t base = (int64_t)blockIdx.x * (IT * 256);
   const int64_t pb = base / ipp;
   const int rb = (int)(base - pb * ipp);
-  const uint16_t* xs[kDirectItems];
-  uint16_t* os[kDirectItems];
-  int64_t cso[kDirectItems];
-  int dls[kDirectItems];
-  bool ok[kDirectItems], qrow[kDirectItems];
+  const uint16_t* xs[IT];
+  uint16_t* os[IT];
+  int64_t cso[IT];
+  int dls[IT];
+  bool ok[IT], qrow[IT];
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
+  for (int u = 0; u < IT; ++u) {
     const int l = u * 256 + (int)threadIdx.x;
     ok[u] = base + l < nitems;
     int j;
@@ -302,24 +360,31 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
     dls[u] = c * VEC;
     cso[u] = b * a.cs_sb + sidx * a.cs_ss;
   }
-  float xl[kDirectItems][VEC], xh[kDirectItems][VEC];
+  // held packed until use (8 registers per half chunk instead of 16)
+  u32x4 rl[IT], rh[IT];
+  ItemTables tb[IT];
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
-    Chunk<VEC>::load(xs[u] + dls[u], xl[u]);
-    Chunk<VEC>::load(xs[u] + half + dls[u], xh[u]);
+  for (int u = 0; u < IT; ++u) {
+    rl[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + dls[u]));
+    rh[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + half + dls[u]));
   }
+  if constexpr (IT == 1)
+    load_item_tables<NORM>(tb[0], a.cos, a.sin, cso[0], dls[0], half, qrow[0] ? a.qw : a.kw);
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
+  for (int u = 0; u < IT; ++u) {
     if (!ok[u]) continue;
-    if constexpr (NORM)
-      rms_norm_chunks(xl[u], xh[u], qrow[u] ? a.qw : a.kw, dls[u], half, a.chunks.d,
-                      1.0 / (double)D, a.eps);
+    if constexpr (IT > 1)
+      load_item_tables<NORM>(tb[u], a.cos, a.sin, cso[u], dls[u], half, qrow[u] ? a.qw : a.kw);
+    float xl[VEC], xh[VEC];
+    unpack8(rl[u], xl);
+    unpack8(rh[u], xh);
+    if constexpr (NORM) rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, a.inv_d, a.eps);
     float cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
-    load_cs8<false>(a.cos, cso[u] + dls[u], cl);
-    load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
-    load_cs8<false>(a.sin, cso[u] + dls[u], sl);
-    load_cs8<false>(a.sin, cso[u] + half + dls[u], sh);
-    rotate<MODE, VEC>(xl[u], xh[u], cl, ch, sl, sh, ol, oh);
+    unpack8(tb[u].cs[0], cl);
+    unpack8(tb[u].cs[1], ch);
+    unpack8(tb[u].cs[2], sl);
+    unpack8(tb[u].cs[3], sh);
+    rotate<MODE, VEC>(xl, xh, cl, ch, sl, sh, ol, oh);
     Chunk<VEC>::store(os[u] + dls[u], ol);
     Chunk<VEC>::store(os[u] + half + dls[u], oh);
   }
@@ -351,6 +416,7 @@ struct KvArgs {
   const uint16_t* qw;    // RMSNorm of q / k head rows (norm kernel only)
   const uint16_t* kw;
   float eps;
+  double inv_d;          // 1 / D
 };
 
 template <bool NORM = false>
@@ -363,16 +429,16 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
   const int64_t nitems = a.B * a.S * ipp;
   const int64_t P = a.pos + (a.pos_dev ? a.pos_dev[0] : 0);
   // block-level decomposition once, per item small divisions (SmallDiv)
-  const int64_t base = (int64_t)blockIdx.x * (kDirectItems * 256);
+  const int64_t base = (int64_t)blockIdx.x * (kKvItems * 256);
   const int64_t pb = base / ipp;
   const int rb = (int)(base - pb * ipp);
-  const uint16_t* xs[kDirectItems];
-  uint16_t* os[kDirectItems];
-  int64_t cso[kDirectItems];
-  int dls[kDirectItems], kind[kDirectItems];  // kind: 0 q, 1 k, 2 v
-  bool ok[kDirectItems];
+  const uint16_t* xs[kKvItems];
+  uint16_t* os[kKvItems];
+  int64_t cso[kKvItems];
+  int dls[kKvItems], kind[kKvItems];  // kind: 0 q, 1 k, 2 v
+  bool ok[kKvItems];
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
+  for (int u = 0; u < kKvItems; ++u) {
     const int l = u * 256 + (int)threadIdx.x;
     ok[u] = base + l < nitems;
     int j;
@@ -406,14 +472,19 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
     dls[u] = c * VEC;
     cso[u] = b * a.cs_sb + sidx * a.cs_ss;
   }
-  u32x4 rl[kDirectItems], rh[kDirectItems];
+  u32x4 rl[kKvItems], rh[kKvItems];
+  ItemTables tb[kKvItems];
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
+  for (int u = 0; u < kKvItems; ++u) {
     rl[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + dls[u]));
     rh[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + half + dls[u]));
   }
 #pragma unroll
-  for (int u = 0; u < kDirectItems; ++u) {
+  for (int u = 0; u < kKvItems; ++u)  // v items load (unused) tables too: no branch
+    load_item_tables<NORM>(tb[u], a.cos, a.sin, cso[u], dls[u], half,
+                           kind[u] == 0 ? a.qw : a.kw);
+#pragma unroll
+  for (int u = 0; u < kKvItems; ++u) {
     if (!ok[u]) continue;
     u32x4* lo = reinterpret_cast<u32x4*>(os[u] + dls[u]);
     u32x4* hi = reinterpret_cast<u32x4*>(os[u] + half + dls[u]);
@@ -426,12 +497,11 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
     unpack8(rl[u], xl);
     unpack8(rh[u], xh);
     if constexpr (NORM)
-      rms_norm_chunks(xl, xh, kind[u] == 0 ? a.qw : a.kw, dls[u], half, a.chunks.d,
-                      1.0 / (double)a.D, a.eps);
-    load_cs8<false>(a.cos, cso[u] + dls[u], cl);
-    load_cs8<false>(a.cos, cso[u] + half + dls[u], ch);
-    load_cs8<false>(a.sin, cso[u] + dls[u], sl);
-    load_cs8<false>(a.sin, cso[u] + half + dls[u], sh);
+      rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, a.inv_d, a.eps);
+    unpack8(tb[u].cs[0], cl);
+    unpack8(tb[u].cs[1], ch);
+    unpack8(tb[u].cs[2], sl);
+    unpack8(tb[u].cs[3], sh);
     rotate<UMIC_ROPE_TEXT, VEC>(xl, xh, cl, ch, sl, sh, ol, oh);
     *lo = pack8(ol);
     *hi = pack8(oh);
@@ -473,7 +543,8 @@ int launch_rope(const RopeArgs& a, bool direct_ok, hipStream_t st) {
   if constexpr (!CS32 && VEC == 8) {
     if (!direct_ok) return launch_staged<MODE, CS32, VEC>(a, st);
     const int64_t nitems = a.B * a.S * (a.Hq + a.Hk) * (a.D / 2 / VEC);
-    const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+    constexpr int per_block = direct_items<false>() * 256;
+    const int64_t blocks = (nitems + per_block - 1) / per_block;
     if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
     hipLaunchKernelGGL((rope_qk_direct_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st,
                        with_divisors<VEC>(a));
@@ -586,7 +657,7 @@ int kv_append_impl(const void* q, const void* k, const void* v, void* q_out, voi
            pos_dev, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh,
            qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss,
            small_div((int)((Hq + 2 * Hk) * (D / 16))), small_div((int)(D / 16)),
-           (const uint16_t*)qw, (const uint16_t*)kw, eps};
+           (const uint16_t*)qw, (const uint16_t*)kw, eps, 1.0 / (double)D};
   bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
             (uintptr_t)sin % 16 == 0;
   if (Hq) {
@@ -606,7 +677,7 @@ int kv_append_impl(const void* q, const void* k, const void* v, void* q_out, voi
   }
   if (!ok) return UMIC_ERR_UNSUPPORTED;
   const int64_t nitems = B * S * (Hq + 2 * Hk) * (D / 16);
-  const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+  const int64_t blocks = (nitems + kKvItems * 256 - 1) / (kKvItems * 256);
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   if (norm)
     hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
@@ -685,8 +756,10 @@ extern "C" int umic_qk_rmsnorm_rope_bf16(const void* q, const void* k, void* q_o
   a.qw = (const uint16_t*)q_w;
   a.kw = (const uint16_t*)k_w;
   a.eps = eps;
+  a.inv_d = 1.0 / (double)D;
   const int64_t nitems = B * S * (Hq + Hk) * (D / 16);
-  const int64_t blocks = (nitems + kDirectItems * 256 - 1) / (kDirectItems * 256);
+  constexpr int per_block = direct_items<true>() * 256;
+  const int64_t blocks = (nitems + per_block - 1) / per_block;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((rope_qk_direct_kernel<UMIC_ROPE_TEXT, true>), dim3((unsigned)blocks),
                      dim3(256), 0, as_stream(stream), a);
