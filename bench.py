@@ -392,21 +392,14 @@ def hbm_ceiling() -> int:
     return 0
 
 
-def layer_step() -> dict:
-    """BASELINE config 5: one Qwen3-VL text decoder layer (hidden 4096, 32 q /
-    8 kv heads, head_dim 128, intermediate 12288, random N(0, 0.02) weights,
-    norms 1 + N(0, 0.1)) timed eager and with the fused path injected
-    (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope,
-    fuse_kv_rope -- with no cache, q_norm / k_norm / RoPE in one launch):
-    prefill at M=3100 and decode at M=1, the decode step also captured in a
-    HIP graph (torch.cuda.CUDAGraph) and replayed, as the reference's decode
-    runner does (src/umic/graph.py:155-167)."""
+def _config5_layer():
+    """BASELINE config 5 text decoder layer in bf16 on the GPU with random
+    N(0, 0.02) weights (norms 1 + N(0, 0.1)), its rotary embedding and the
+    generator that drew them."""
     import torch
     from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
     from transformers.models.qwen3_vl.modeling_qwen3_vl import (Qwen3VLTextDecoderLayer,
                                                                 Qwen3VLTextRotaryEmbedding)
-
-    from umic import integrate
 
     cfg = Qwen3VLTextConfig(hidden_size=4096, intermediate_size=12288, num_hidden_layers=1,
                             num_attention_heads=32, num_key_value_heads=8, head_dim=128,
@@ -421,6 +414,52 @@ def layer_step() -> dict:
             else:
                 prm.copy_(0.02 * torch.randn(prm.shape, generator=gen, device="cuda"))
     rot = Qwen3VLTextRotaryEmbedding(cfg).to("cuda")
+    return layer, rot, gen
+
+
+def decode_layer() -> int:
+    """Ten fused decode steps (one row) of the config-5 layer, every fuse_*
+    of apply() injected, for a kernel trace of the decode step
+    (``rocprofv3 --kernel-trace --stats -- python bench.py --decode-layer``):
+    the GEMM sites run on the library's GEMV, norms and RoPE fused."""
+    import torch
+
+    from umic import _lib, integrate
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    layer, rot, gen = _config5_layer()
+    h = _bf(1, 1, 4096, gen=gen)
+    cs = rot(h, torch.arange(1, device="cuda")[None])
+    with torch.no_grad():
+        integrate.fuse_mlps(layer)
+        integrate.fuse_linears(layer)
+        integrate.fuse_rmsnorms(layer)
+        integrate.fuse_add_rmsnorm(layer)
+        integrate.fuse_text_rope()
+        integrate.fuse_kv_rope(layer)
+        for i in range(13):
+            layer(h, position_embeddings=cs)
+            torch.cuda.synchronize()
+            if i >= 3:
+                print(f"decode step {i - 3} done", flush=True)
+    return 0
+
+
+def layer_step() -> dict:
+    """BASELINE config 5: one Qwen3-VL text decoder layer (hidden 4096, 32 q /
+    8 kv heads, head_dim 128, intermediate 12288, random N(0, 0.02) weights,
+    norms 1 + N(0, 0.1)) timed eager and with the fused path injected
+    (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope,
+    fuse_kv_rope -- with no cache, q_norm / k_norm / RoPE in one launch):
+    prefill at M=3100 and decode at M=1, the decode step also captured in a
+    HIP graph (torch.cuda.CUDAGraph) and replayed, as the reference's decode
+    runner does (src/umic/graph.py:155-167)."""
+    import torch
+
+    from umic import integrate
+
+    layer, rot, gen = _config5_layer()
     inputs = {}
     for M in (3100, 1):
         h = _bf(1, M, 4096, gen=gen)
@@ -614,6 +653,8 @@ def main() -> int:
                     help="HBM read / write / copy ceilings from the csrc/probes program")
     ap.add_argument("--vit-sites", action="store_true",
                     help="time the ViT projection sites, this library against hipBLASLt")
+    ap.add_argument("--decode-layer", action="store_true",
+                    help="run ten fused config-5 decode steps (for a kernel trace) and exit")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the decoder-layer (config 5) prefill/decode timing")
     ap.add_argument("--no-kv-cache", action="store_true",
@@ -634,6 +675,8 @@ def main() -> int:
         return hbm_ceiling()
     if args.vit_sites:
         return vit_sites()
+    if args.decode_layer:
+        return decode_layer()
 
     import torch
 

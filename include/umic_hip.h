@@ -211,6 +211,9 @@ int umic_qk_rmsnorm_rope_kv_append_bf16(const void* q, const void* k, const void
  * UMIC_ACT_GELU_TANH (no counterpart in the reference: the tanh GELU of the
  * Qwen3-VL ViT MLP); the bias add and the activation run in fp32 on the
  * accumulator, one bf16 rounding.  Any other act: UMIC_ERR_INVALID_ARG.
+ * M <= 8 (decode) runs a weight-streaming GEMV kernel instead of the MFMA
+ * tiles; same arguments, results and epilogue numerics (fp32 sums in
+ * another order).
  * Requires K % 32 == 0, N % 8 == 0, ldx/ldw/ldo % 8 == 0 and 16-byte
  * aligned pointers (else UMIC_ERR_UNSUPPORTED).
  * Replaces: kernels/linear.py:118-145 (linear_triton), kernel
@@ -252,7 +255,8 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
  * Fused P5 MLP front half: out = silu(x @ wg^T) * (x @ wu^T), one bf16
  * rounding of the fp32 product.  wg, wu: [N, K] nn.Linear weights (the
  * reference passes them as .t() views; same memory).
- * Same shape / alignment rules as umic_linear_bf16.
+ * Same shape / alignment rules, and the same M <= 8 GEMV path, as
+ * umic_linear_bf16.
  * Replaces: kernels/fused_ffn.py:93-126 (gate_silu_mul_triton /
  * gate_silu_mul), kernel kernels/fused_ffn.py:48-91; caller
  * integrate.py:44-55.

@@ -3,8 +3,8 @@ injection (hidden 4096, 32 q / 8 kv heads, head_dim 128,
 intermediate 12288, random N(0, 0.02) weights, norms 1 + N(0, 0.1)).
 
 Prefill (M=3100) must take every fused kernel -- checked by counting the C-ABI
-calls -- and decode (M=1) must keep the GEMM sites on the vendor path
-(FUSE_MIN_ROWS) while norms and RoPE stay fused.  Outputs are compared with the
+calls -- and decode (M=1) takes the library's GEMV for the same GEMM sites
+(GEMV_MAX_ROWS) while norms and RoPE stay fused.  Outputs are compared with the
 unpatched layer on the same GPU within the GEMM tolerance.
 """
 
@@ -64,7 +64,8 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
     assert call_log["umic_rmsnorm_bf16"] == 3          # input_layernorm, q_norm, k_norm
     assert call_log["umic_add_rmsnorm_bf16"] == 1
     assert call_log["umic_rope_qk_bf16"] == 1          # q and k in one launch
-    gemm_calls = 1 if M >= integrate.FUSE_MIN_ROWS else 0
+    # the tiled kernels at prefill, the GEMV at decode (one row)
+    gemm_calls = 1 if M >= integrate.FUSE_MIN_ROWS or M <= integrate.GEMV_MAX_ROWS else 0
     assert call_log["umic_gate_silu_mul_bf16"] == gemm_calls
     # q_proj, o_proj and, at prefill (stream-K shape), the MLP's down_proj,
     # all through the workspace entry point

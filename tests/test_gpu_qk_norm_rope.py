@@ -8,8 +8,9 @@ every [D] head row, then ``rope_text`` -- the eager chain
 (transformers modeling_qwen3_vl ``Qwen3VLTextAttention.forward``).  Checked
 bit for bit at the BASELINE text shapes (config 5's 3094-token prefill, its
 32-token flow step, a decode token), a batch of two with per-sequence
-tables, and the smallest head sizes the kernels take (D = 16 and 32: one and
-two lanes per head row).  Weights are random, not ones, so a dropped or
+tables or one table broadcast over the batch, and head sizes from the
+smallest the kernels take (D = 16: one lane per head row) to the largest
+(D = 1024: one row per wave), through every step of the row reduction.  Weights are random, not ones, so a dropped or
 swapped q/k weight fails.
 """
 
@@ -39,6 +40,9 @@ SHAPES = [
     (2, 5, 4, 2, 64),          # batch of two, per-sequence tables
     (1, 9, 3, 1, 16),          # one lane per head row
     (1, 7, 2, 2, 32),          # two lanes per head row
+    (1, 5, 2, 1, 256),         # 16 lanes: the full-row DPP mirror
+    (1, 3, 2, 1, 512),         # 32 lanes: DPP, then a shuffle
+    (1, 2, 1, 1, 1024),        # 64 lanes: the whole wave is one row
 ]
 
 
@@ -65,6 +69,24 @@ def test_qk_norm_rope_vs_oracle(B, S, Hq, Hk, D):
     qn, kn = bits(normed(qs, qw)), bits(normed(ks, kw))
     for b in range(B):
         c, s = bits(cos)[b], bits(sin)[b]
+        assert np.array_equal(bits(qo.transpose(1, 2))[b], oracle.rope_text(qn[b], c, s)), b
+        assert np.array_equal(bits(ko.transpose(1, 2))[b], oracle.rope_text(kn[b], c, s)), b
+
+
+def test_qk_norm_rope_broadcast_tables():
+    """B = 2 against one [1, S, D] table broadcast over the batch (HF passes
+    such tables when every sequence shares its positions)."""
+    B, S, Hq, Hk, D = 2, 40, 4, 2, 128
+    qs, ks, _, _, _ = inputs(B, S, Hq, Hk, D, 1, seed=31)
+    qw, kw = weights(D, seed=32)
+    cos, sin = tables(1, S, D, 17)
+    q, k = (t.to(DEV).transpose(1, 2) for t in (qs, ks))
+    assert rope.qk_norm_rope_eligible(q, k, cos.to(DEV), sin.to(DEV), qw.to(DEV), kw.to(DEV))
+    qo, ko = rope.qk_norm_rope(q, k, cos.to(DEV), sin.to(DEV), qw.to(DEV), kw.to(DEV), EPS)
+    torch.cuda.synchronize()
+    qn, kn = bits(normed(qs, qw)), bits(normed(ks, kw))
+    c, s = bits(cos)[0], bits(sin)[0]
+    for b in range(B):
         assert np.array_equal(bits(qo.transpose(1, 2))[b], oracle.rope_text(qn[b], c, s)), b
         assert np.array_equal(bits(ko.transpose(1, 2))[b], oracle.rope_text(kn[b], c, s)), b
 
@@ -103,6 +125,7 @@ def test_qk_norm_rope_vs_transformers():
     (1, 1, 32, 8, 128, 3126, 3200),      # decode token
     (2, 5, 4, 2, 64, 7, 16),             # batch of two
     (1, 9, 3, 1, 16, 0, 9),              # exactly fills the cache, D = 16
+    (1, 6, 2, 1, 256, 3, 12),            # 16 lanes per head row
 ])
 def test_qk_norm_rope_kv_append_vs_oracle(B, S, Hq, Hk, D, pos, L):
     print(f"qk_norm_rope_kv_append B={B} S={S} Hq={Hq} Hk={Hk} D={D} pos={pos} L={L}",

@@ -168,7 +168,9 @@ def test_cpu_patched_vision_model_is_bit_identical():
 # ---- FUSE_MIN_ROWS regime dispatch ----------------------------------------
 
 def test_fuse_min_rows_boundary(monkeypatch):
-    """63 rows run the eager class forward; 64 rows take the fused kernel."""
+    """63 rows run the eager class forward; 64 rows take the fused kernel;
+    decode-sized calls (up to GEMV_MAX_ROWS rows) take the library's GEMV,
+    the MLP's down projection included, and one row more is eager again."""
     calls = []
 
     def fake_p5(x, wg_kn, wu_kn):
@@ -187,13 +189,13 @@ def test_fuse_min_rows_boundary(monkeypatch):
     integrate.fuse_mlps(m)
     integrate.fuse_linears(m)
     mlp, q = m.layers[0].mlp, m.layers[0].self_attn.q_proj
-    for rows in (63, 64):
+    for rows in (8, 9, 63, 64):
         x = torch.randn(1, rows, 128).to(BF)
         with torch.no_grad():
             mlp(x)
             q(x)
-    assert calls == [("p5", 64), ("lin", 64)]
-    assert integrate.FUSE_MIN_ROWS == 64
+    assert calls == [("p5", 8), ("lin", 8), ("lin", 8), ("p5", 64), ("lin", 64)]
+    assert integrate.FUSE_MIN_ROWS == 64 and integrate.GEMV_MAX_ROWS == 8
 
 
 def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):

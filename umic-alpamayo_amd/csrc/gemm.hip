@@ -669,8 +669,164 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
   }
 }
 
+// ---- Few-row (decode) path --------------------------------------------
+//
+// With M <= kGemvMaxRows the product is a weight stream: every weight byte is
+// used M times, so MFMA tiles (one 256-row x tile mostly padding) waste the
+// machine; hipBLASLt's GEMV kernels reach 0.6-3.6 TB/s on the config-5
+// decode shapes (N = 1024 .. 12288, K = 4096 / 12288).  Here one workgroup
+// owns kGemvCols consecutive output columns and streams their weight rows
+// (for P5: the gate and the up row of each column) in 1 KB coalesced wave
+// loads; its kGemvWaves waves split K (slab j of 64 16-byte chunks goes to
+// wave j mod kGemvWaves), so even N = 1024 gives 2048 waves, 8 per CU, and
+// each lane keeps U slabs in flight.  x rows are re-read per slab from L2
+// (at most 8 x 24 KB).  fp32 FMAs per lane, a butterfly over the 64 lanes,
+// the four waves' partials summed through LDS, then the GEMM's epilogue
+// (bias, GELU, silu(g) * u) and one bf16 rounding.
+constexpr int kGemvMaxRows = 8;
+constexpr int kGemvCols = 2;
+constexpr int kGemvWaves = 4;  // per 256-thread workgroup
+
+template <int NB, int ACT, bool BIAS>
+__device__ __forceinline__ float gemv_epilogue(float v, float u, float bias) {
+  if constexpr (NB == 2) {
+    // as the GEMM epilogue: silu(g) * u with the hardware exp2 / reciprocal
+    const float den = 1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(den) * u;
+  } else {
+    if constexpr (BIAS) v = v + bias;
+    if constexpr (ACT == UMIC_ACT_GELU) v = gelu_erf(v);
+    if constexpr (ACT == UMIC_ACT_GELU_TANH) v = gelu_tanh(v);
+    return v;
+  }
+}
+
+template <int NB, int ACT, bool BIAS, int MR>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g) {
+  constexpr int R = kGemvCols;
+  constexpr int U = MR <= 2 ? 4 : 2;
+  __shared__ float part[kGemvWaves][MR * NB * R];
+  const int lane = (int)threadIdx.x & 63;
+  const int wave = (int)threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * R;  // the launch covers N exactly
+  const int64_t chunks = g.K / 8;
+  // Columns past N (when N % R != 0) and x rows past M re-read the last
+  // valid row; their results are not stored.
+  const uint16_t* wr[NB][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = n0 + r < g.N ? n0 + r : g.N - 1;
+    wr[0][r] = g.w0 + n * g.ldw0;
+    if constexpr (NB == 2) wr[NB - 1][r] = g.w1 + n * g.ldw1;
+  }
+  const uint16_t* xr[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xr[m] = g.x + (m < g.M ? m : g.M - 1) * g.ldx;
+  float acc[MR][NB][R];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][b][r] = 0.0f;
+  for (int64_t c0 = lane + (int64_t)64 * U * wave; c0 < chunks; c0 += 64 * U * kGemvWaves) {
+    u32x4 wv[U][NB][R], xv[U][MR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + 64 * u < chunks ? c0 + 64 * u : c0;  // c0 < chunks
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          wv[u][b][r] = ld_stream(reinterpret_cast<const u32x4*>(wr[b][r] + c * 8));
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xv[u][m] = *reinterpret_cast<const u32x4*>(xr[m] + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + 64 * u >= chunks) break;
+      float xf[MR][8];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) unpack8(xv[u][m], xf[m]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float wf[8];
+          unpack8(wv[u][b][r], wf);
+#pragma unroll
+          for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[m][b][r] = __builtin_fmaf(wf[e], xf[m][e], acc[m][b][r]);
+        }
+    }
+  }
+  // every lane ends with the column totals
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) acc[m][b][r] += __shfl_xor(acc[m][b][r], s, kWave);
+  // the waves' K parts, summed in a fixed order by wave 0
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[wave][(m * NB + b) * R + r] = acc[m][b][r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float t = part[0][(m * NB + b) * R + r];
+#pragma unroll
+        for (int w = 1; w < kGemvWaves; ++w) t += part[w][(m * NB + b) * R + r];
+        acc[m][b][r] = t;
+      }
+  // lane m stores row m (static indices: a select per row, no dynamic
+  // register indexing)
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (lane != m || m >= g.M) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = n0 + r;
+      if (n >= g.N) continue;
+      const float bias = BIAS ? bf2f(g.bias[n]) : 0.0f;
+      const float o = gemv_epilogue<NB, ACT, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
+      g.out[m * g.ldo + n] = (uint16_t)f2bf(o);
+    }
+  }
+}
+
+template <int NB, int ACT, bool BIAS>
+int launch_gemv(const GemmArgs& g, hipStream_t st) {
+  const int64_t grid = (g.N + kGemvCols - 1) / kGemvCols;  // one workgroup per column group
+  if (grid > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  const dim3 gd((unsigned)grid), bd(kGemvWaves * 64);
+  if (g.M <= 1)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, g);
+  else if (g.M <= 2)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, g);
+  else if (g.M <= 4)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, g);
+  else
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, g);
+  return launch_status();
+}
+
 template <int NB, int ACT, bool BIAS>
 int launch_gemm(GemmArgs g, hipStream_t st) {
+  if (g.M <= kGemvMaxRows) return launch_gemv<NB, ACT, BIAS>(g, st);
   const int64_t bn = NB == 1 ? kBW : kBW / 2;
   const int64_t tm = (g.M + kBM - 1) / kBM;
   const int64_t tn = (g.N + bn - 1) / bn;
@@ -717,7 +873,7 @@ struct SkPlan {
 // keeps at least kSkMinSteps steps.
 SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   SkPlan pl{0, 0, 0, 0, 0, 0};
-  if (M <= 0 || N <= 0 || K <= 0 || K % kBK) return pl;
+  if (M <= kGemvMaxRows || N <= 0 || K <= 0 || K % kBK) return pl;  // few rows: the GEMV
   const int64_t cus = device_cus();
   const int64_t T = ((M + kBM - 1) / kBM) * ((N + kBW - 1) / kBW);
   const int64_t KT = K / kBK;

@@ -11,7 +11,8 @@ hooks, and deleting the attribute restores the class forward.
 
 Each replacement forward first decides whether the fused gfx950 kernel
 reproduces the module on the given inputs (GPU bf16 tensors of a handled
-layout; for the GEMM sites also at least FUSE_MIN_ROWS rows; and no
+layout; for the GEMM sites also at least FUSE_MIN_ROWS rows, or at most
+GEMV_MAX_ROWS (the decode GEMV); and no
 gradient to carry, since the kernels have no backward).  If not, it runs
 the module's own class forward -- the original eager math on whatever
 device the inputs live on, recorded by autograd as usual.  If the inputs are eligible but libumic_hip.so
@@ -39,6 +40,28 @@ _SILU_NAMES = ("silu", "swish")
 # (reference src/umic/integrate.py:27-30).  Norms and RoPE have no floor:
 # one fused launch always replaces several eager ones.
 FUSE_MIN_ROWS = 64
+
+# ...except for the fewest rows, the decode steps: with 1..GEMV_MAX_ROWS
+# rows the library's entry points run a weight-streaming GEMV kernel that
+# measured 2-4x hipBLASLt's GEMVs on the config-5 decode shapes, so the text
+# MLP and projections take it there (P5 with its silu(g) * u epilogue, the
+# down projection, q/k/v/o).  Between the two bounds the vendor path stays.
+GEMV_MAX_ROWS = 8
+
+
+def _gemm_rows_ok(x: torch.Tensor) -> bool:
+    """Row count in one of the fused GEMM regimes (GEMV or tiled)."""
+    rows = _rows(x)
+    return rows >= FUSE_MIN_ROWS or 1 <= rows <= GEMV_MAX_ROWS
+
+
+def _linear(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """mod(x) for an nn.Linear, on the library's GEMV in the decode regime."""
+    if (isinstance(mod, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS
+            and linear.linear_eligible(x, mod.weight, mod.bias)
+            and not grad_needed(x, mod.weight, mod.bias)):
+        return linear.linear_hip(x, mod.weight, mod.bias)
+    return mod(x)
 
 # Projection sites routed to the fused linear (reference integrate.py:91).
 INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
@@ -90,13 +113,15 @@ def _is_p5_mlp(module: nn.Module) -> bool:
 def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """P5-fused replacement: silu(x@Wg)*(x@Wu) in one kernel, then down."""
     wg, wu = self.gate_proj.weight, self.up_proj.weight
-    if (_rows(x) < FUSE_MIN_ROWS or not fused_ffn.p5_eligible(x, wg, wu)
+    if (not _gemm_rows_ok(x) or not fused_ffn.p5_eligible(x, wg, wu)
             or grad_needed(x, wg, wu)):
         return _eager(self, x)
     # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
     # takes -- the kernel reads the original weight memory.
     h = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
     down = self.down_proj
+    if _rows(h) <= GEMV_MAX_ROWS:
+        return _linear(down, h)
     if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear)
             and linear.linear_eligible(h, down.weight, down.bias)
             and linear.stream_k_planned(h, down.weight)):
@@ -126,8 +151,9 @@ def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
 # ---------------------------------------------------------------------------
 
 def _patched_linear_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    """Route large-M calls to the fused linear; GEMV stays on the vendor BLAS."""
-    if (_rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, self.weight, self.bias)
+    """Route large-M and decode calls to the fused linear (tiled or GEMV);
+    the rows between stay on the vendor BLAS."""
+    if (not _gemm_rows_ok(x) or not linear.linear_eligible(x, self.weight, self.bias)
             or grad_needed(x, self.weight, self.bias)):
         return _eager(self, x)
     return linear.linear_hip(x, self.weight, self.bias)
@@ -670,9 +696,9 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
             layer = None
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    q_raw = self.q_proj(hidden_states).view(hidden_shape)
-    k_raw = self.k_proj(hidden_states).view(hidden_shape)
-    v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    q_raw = _linear(self.q_proj, hidden_states).view(hidden_shape)
+    k_raw = _linear(self.k_proj, hidden_states).view(hidden_shape)
+    v = _linear(self.v_proj, hidden_states).view(hidden_shape).transpose(1, 2)
     cos, sin = position_embeddings
     q, k = q_raw.transpose(1, 2), k_raw.transpose(1, 2)
     norm = _head_norms(self, q)
@@ -700,7 +726,7 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
     out, weights = attn(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling,
                         **kwargs)
     out = out.reshape(*input_shape, -1).contiguous()
-    return self.o_proj(out), weights
+    return _linear(self.o_proj, out), weights
 
 
 def fuse_kv_rope(model: nn.Module, dry_run: bool = False) -> int:
