@@ -252,6 +252,23 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
                         int act, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Up to three linears over one x in one launch, the decode GEMV path only:
+ * out_i = act(x @ w_i^T + bias_i) for i < count (count 1..3), each with its
+ * own N_i, weight leading dim ldw_i and output leading dim ldo_i; bias may
+ * be NULL, or an array whose entries may be NULL.  M must be 1..8 (else
+ * UMIC_ERR_UNSUPPORTED; M == 0 is a no-op); shape and alignment rules are
+ * umic_linear_bf16's, per segment.  Results equal umic_linear_bf16 on each
+ * linear (the same kernel and summation order).
+ * No counterpart in the reference, which runs the text attention's q_proj,
+ * k_proj and v_proj (transformers modeling_qwen3_vl
+ * Qwen3VLTextAttention.forward) as three vendor GEMVs at decode.
+ */
+int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int count,
+                           const void* const* w, const void* const* bias, void* const* out,
+                           const int64_t* N, const int64_t* ldw, const int64_t* ldo, int act,
+                           void* stream);
+
+/*
  * Fused P5 MLP front half: out = silu(x @ wg^T) * (x @ wu^T), one bf16
  * rounding of the fp32 product.  wg, wu: [N, K] nn.Linear weights (the
  * reference passes them as .t() views; same memory).

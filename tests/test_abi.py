@@ -36,6 +36,7 @@ def test_header_declares_expected_entry_points():
     for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
               "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
               "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
+              "umic_linear_multi_bf16",
               "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
               "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_version", "umic_error_string"):
         assert n in names
@@ -163,6 +164,29 @@ def test_qk_norm_rope_rejection(lib):
     assert g(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1e-6, 1, 4, 4, 1, 80,
              *kv[:12], 8 * 4096 * 80, 4096 * 80, 80, 100, 0, None, 80, 80,
              None) == E_UNS                                             # 80/16 = 5
+
+
+def test_linear_multi_rejection(lib):
+    """Argument checks of the multi-linear decode GEMV, before any launch."""
+    import ctypes
+
+    E_ARG, E_UNS = -1, -2
+    f = lib.umic_linear_multi_bf16
+    fake = 1 << 20
+    P3 = ctypes.c_void_p * 3
+    I3 = ctypes.c_int64 * 3
+    w, out = P3(fake, fake, fake), P3(fake, fake, fake)
+    N, ldw, ldo = I3(64, 16, 16), I3(128, 128, 128), I3(64, 16, 16)
+    assert f(fake, 0, 128, 128, 3, w, None, out, N, ldw, ldo, 0, None) == 0   # M = 0: no-op
+    assert f(fake, 1, 128, 128, 0, w, None, out, N, ldw, ldo, 0, None) == E_ARG
+    assert f(fake, 1, 128, 128, 4, w, None, out, N, ldw, ldo, 0, None) == E_ARG
+    assert f(fake, 1, 128, 128, 3, w, None, out, N, ldw, ldo, 5, None) == E_ARG  # act
+    assert f(fake, 9, 128, 128, 3, w, None, out, N, ldw, ldo, 0, None) == E_UNS  # not decode
+    assert f(fake, 1, 80, 128, 3, w, None, out, N, ldw, ldo, 0, None) == E_UNS   # K % 32
+    assert f(fake, 1, 128, 128, 3, w, None, out, I3(64, -1, 16), ldw, ldo, 0, None) == E_ARG
+    assert f(fake, 1, 128, 128, 3, w, None, out, N, I3(128, 64, 128), ldo, 0, None) == E_ARG
+    assert f(fake, 1, 128, 128, 3, P3(fake, fake + 2, fake), None, out, N, ldw, ldo, 0,
+             None) == E_UNS                                             # misaligned w
 
 
 def test_wrappers_refuse_cpu_tensors():

@@ -125,3 +125,35 @@ def test_gemv_p5_decode_shape_vs_fp32():
     e1, e2 = max_rel_err(y, ref), rel_err(y, ref)
     print(f"gemv P5 decode: max_rel {e1:.2e} rel {e2:.2e}", flush=True)
     assert e1 <= TOL and e2 <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_linear_multi_equals_single_linears(M):
+    """umic_linear_multi_bf16 over q/k/v-shaped linears (N 4096, 1024, 1024;
+    a bias on one of them) equals umic_linear_bf16 on each, bit for bit, and
+    the oracle to one ulp almost everywhere."""
+    g = torch.Generator().manual_seed(90 + M)
+    K = 1024
+    x = bf16_randn(M, K, gen=g).to(DEV)
+    ws = [bf16_randn(N, K, scale=0.05, gen=g).to(DEV) for N in (4096, 1024, 1024)]
+    bs = [None, bf16_randn(1024, scale=0.5, gen=g).to(DEV), None]
+    outs = linear.linear_multi_hip(x, ws, bs)
+    singles = [linear.linear_hip(x, w, b) for w, b in zip(ws, bs)]
+    torch.cuda.synchronize()
+    for o, r, w, b in zip(outs, singles, ws, bs):
+        assert o.shape == r.shape and torch.equal(o, r)
+        _check_vs_oracle(o, oracle.linear(bits(x), bits(w), None if b is None else bits(b), 0,
+                                          fused=True))
+
+
+def test_linear_multi_empty_segment_and_rows_bound():
+    g = torch.Generator().manual_seed(99)
+    x = bf16_randn(2, 256, gen=g).to(DEV)
+    w0, w2 = bf16_randn(64, 256, gen=g).to(DEV), bf16_randn(32, 256, gen=g).to(DEV)
+    empty = torch.empty(0, 256, dtype=torch.bfloat16, device=DEV)
+    o0, o1, o2 = linear.linear_multi_hip(x, [w0, empty, w2])
+    torch.cuda.synchronize()
+    assert o1.shape == (2, 0)
+    assert torch.equal(o0, linear.linear_hip(x, w0)) and torch.equal(o2, linear.linear_hip(x, w2))
+    with pytest.raises(ValueError):
+        linear.linear_multi_hip(bf16_randn(9, 256, gen=g).to(DEV), [w0])

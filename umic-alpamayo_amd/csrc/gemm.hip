@@ -701,14 +701,40 @@ __device__ __forceinline__ float gemv_epilogue(float v, float u, float bias) {
   }
 }
 
+// Up to kGemvMaxSegs linears over one x in one launch (the attention's
+// q/k/v projections at decode): segment i owns workgroups [first[i],
+// first[i + 1]) and its own weight, bias, output, N and leading dims.  A
+// single linear (or P5, whose gate/up pair lives in GemmArgs) is one segment.
+constexpr int kGemvMaxSegs = 3;
+struct GemvSegs {
+  const uint16_t* w[kGemvMaxSegs];
+  const uint16_t* bias[kGemvMaxSegs];
+  uint16_t* out[kGemvMaxSegs];
+  int64_t N[kGemvMaxSegs], ldw[kGemvMaxSegs], ldo[kGemvMaxSegs];
+  int64_t first[kGemvMaxSegs + 1];
+  int count;
+};
+
 template <int NB, int ACT, bool BIAS, int MR>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g, GemvSegs sg) {
+  int seg = 0;  // launch-uniform per workgroup
+#pragma unroll
+  for (int i = 1; i < kGemvMaxSegs; ++i)
+    if (i < sg.count && (int64_t)blockIdx.x >= sg.first[i]) seg = i;
+  if (sg.count > 1) {
+    g.w0 = g.w1 = sg.w[seg];
+    g.bias = sg.bias[seg];
+    g.out = sg.out[seg];
+    g.N = sg.N[seg];
+    g.ldw0 = g.ldw1 = sg.ldw[seg];
+    g.ldo = sg.ldo[seg];
+  }
   constexpr int R = kGemvCols;
   constexpr int U = MR <= 2 ? 4 : 2;
   __shared__ float part[kGemvWaves][MR * NB * R];
   const int lane = (int)threadIdx.x & 63;
   const int wave = (int)threadIdx.x >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * R;  // the launch covers N exactly
+  const int64_t n0 = ((int64_t)blockIdx.x - sg.first[seg]) * R;  // each segment covers its N
   const int64_t chunks = g.K / 8;
   // Columns past N (when N % R != 0) and x rows past M re-read the last
   // valid row; their results are not stored.
@@ -801,7 +827,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g) {
     for (int r = 0; r < R; ++r) {
       const int64_t n = n0 + r;
       if (n >= g.N) continue;
-      const float bias = BIAS ? bf2f(g.bias[n]) : 0.0f;
+      const float bias = BIAS && g.bias ? bf2f(g.bias[n]) : 0.0f;
       const float o = gemv_epilogue<NB, ACT, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
       g.out[m * g.ldo + n] = (uint16_t)f2bf(o);
     }
@@ -809,19 +835,30 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g) {
 }
 
 template <int NB, int ACT, bool BIAS>
-int launch_gemv(const GemmArgs& g, hipStream_t st) {
-  const int64_t grid = (g.N + kGemvCols - 1) / kGemvCols;  // one workgroup per column group
-  if (grid > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+int launch_gemv_segs(const GemmArgs& g, const GemvSegs& sg, hipStream_t st) {
+  const int64_t grid = sg.first[sg.count];
+  if (grid <= 0 || grid > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   const dim3 gd((unsigned)grid), bd(kGemvWaves * 64);
   if (g.M <= 1)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, g, sg);
   else if (g.M <= 2)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, g, sg);
   else if (g.M <= 4)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, g, sg);
   else
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, g);
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, g, sg);
   return launch_status();
+}
+
+// One linear (or the P5 pair) as a single segment: one workgroup per
+// kGemvCols output columns.
+template <int NB, int ACT, bool BIAS>
+int launch_gemv(const GemmArgs& g, hipStream_t st) {
+  GemvSegs sg{};
+  sg.count = 1;
+  sg.first[0] = 0;
+  sg.first[1] = (g.N + kGemvCols - 1) / kGemvCols;
+  return launch_gemv_segs<NB, ACT, BIAS>(g, sg, st);
 }
 
 template <int NB, int ACT, bool BIAS>
@@ -997,4 +1034,53 @@ extern "C" int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void
   GemmArgs g{(const uint16_t*)x, (const uint16_t*)wg, (const uint16_t*)wu, nullptr,
              (uint16_t*)out, M, N, K, ldx, ldwg, ldwu, ldo, 0, 0};
   return launch_gemm<2, UMIC_ACT_NONE, false>(g, as_stream(stream));
+}
+
+extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int count,
+                                      const void* const* w, const void* const* bias,
+                                      void* const* out, const int64_t* N, const int64_t* ldw,
+                                      const int64_t* ldo, int act, void* stream) {
+  if (M < 0 || K < 0 || count < 1 || count > kGemvMaxSegs) return UMIC_ERR_INVALID_ARG;
+  if (!w || !out || !N || !ldw || !ldo) return UMIC_ERR_INVALID_ARG;
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
+    return UMIC_ERR_INVALID_ARG;
+  for (int i = 0; i < count; ++i)
+    if (N[i] < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0) return UMIC_OK;
+  if (M > kGemvMaxRows) return UMIC_ERR_UNSUPPORTED;
+  if (!x || ldx < K) return UMIC_ERR_INVALID_ARG;
+  if (K == 0) return UMIC_ERR_UNSUPPORTED;
+  GemvSegs sg{};
+  sg.count = count;
+  bool any_bias = false;
+  int64_t first = 0;
+  for (int i = 0; i < count; ++i) {
+    sg.first[i] = first;
+    if (N[i] == 0) continue;  // empty segment: no workgroups, pointers unused
+    if (!w[i] || !out[i] || ldw[i] < K || ldo[i] < N[i]) return UMIC_ERR_INVALID_ARG;
+    if (!gemm_shape_ok(x, w[i], w[i], out[i], M, N[i], K, ldx, ldw[i], ldw[i], ldo[i]))
+      return UMIC_ERR_UNSUPPORTED;
+    const void* b = bias ? bias[i] : nullptr;
+    if (b && ((uintptr_t)b & 7u)) return UMIC_ERR_UNSUPPORTED;
+    any_bias = any_bias || b;
+    sg.w[i] = (const uint16_t*)w[i];
+    sg.bias[i] = (const uint16_t*)b;
+    sg.out[i] = (uint16_t*)out[i];
+    sg.N[i] = N[i];
+    sg.ldw[i] = ldw[i];
+    sg.ldo[i] = ldo[i];
+    first += (N[i] + kGemvCols - 1) / kGemvCols;
+  }
+  sg.first[count] = first;
+  if (first == 0) return UMIC_OK;
+  GemmArgs g{(const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, M, 0, K, ldx, 0, 0, 0, 0, 0};
+  hipStream_t st = as_stream(stream);
+  if (act == UMIC_ACT_GELU)
+    return any_bias ? launch_gemv_segs<1, UMIC_ACT_GELU, true>(g, sg, st)
+                    : launch_gemv_segs<1, UMIC_ACT_GELU, false>(g, sg, st);
+  if (act == UMIC_ACT_GELU_TANH)
+    return any_bias ? launch_gemv_segs<1, UMIC_ACT_GELU_TANH, true>(g, sg, st)
+                    : launch_gemv_segs<1, UMIC_ACT_GELU_TANH, false>(g, sg, st);
+  return any_bias ? launch_gemv_segs<1, UMIC_ACT_NONE, true>(g, sg, st)
+                  : launch_gemv_segs<1, UMIC_ACT_NONE, false>(g, sg, st);
 }

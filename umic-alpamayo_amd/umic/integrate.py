@@ -649,6 +649,17 @@ def _attention_interface(module: nn.Module):
     return ALL_ATTENTION_FUNCTIONS.get_interface(impl, eager)
 
 
+def _qkv(attn: nn.Module, x: torch.Tensor) -> list[torch.Tensor]:
+    """The attention's q/k/v projections of x: in the decode regime one GEMV
+    launch for all three (umic_linear_multi_bf16), else each on its own."""
+    mods = (attn.q_proj, attn.k_proj, attn.v_proj)
+    if (1 <= _rows(x) <= GEMV_MAX_ROWS and all(isinstance(m, nn.Linear) for m in mods)
+            and all(linear.linear_eligible(x, m.weight, m.bias) for m in mods)
+            and not grad_needed(x, *(m.weight for m in mods), *(m.bias for m in mods))):
+        return linear.linear_multi_hip(x, [m.weight for m in mods], [m.bias for m in mods])
+    return [_linear(m, x) for m in mods]
+
+
 def _head_norms(module: nn.Module, q: torch.Tensor):
     """``(q_w, k_w, eps)`` when the attention's q_norm / k_norm are RMSNorms
     (class name contains "rmsnorm", 1-D weight, one eps) that the fused
@@ -696,9 +707,8 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
             layer = None
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    q_raw = _linear(self.q_proj, hidden_states).view(hidden_shape)
-    k_raw = _linear(self.k_proj, hidden_states).view(hidden_shape)
-    v = _linear(self.v_proj, hidden_states).view(hidden_shape).transpose(1, 2)
+    q_raw, k_raw, v = (t.view(hidden_shape) for t in _qkv(self, hidden_states))
+    v = v.transpose(1, 2)
     cos, sin = position_embeddings
     q, k = q_raw.transpose(1, 2), k_raw.transpose(1, 2)
     norm = _head_norms(self, q)

@@ -10,6 +10,8 @@ lives in umic.integrate, as in the reference.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from umic import _lib
@@ -77,6 +79,41 @@ def linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
                   _ACT_CODES[act],
                   _lib.ptr(ws), ws_bytes, stream)
     return out.reshape(*shape[:-1], N)
+
+
+GEMV_MAX_ROWS = 8  # rows the decode GEMV (and umic_linear_multi_bf16) takes
+
+
+def linear_multi_hip(x: torch.Tensor, weights, biases=None) -> list[torch.Tensor]:
+    """[x @ w.T + b for each (w, b)] in one launch (umic_linear_multi_bf16):
+    the decode GEMV over up to three linears that share x, e.g. the
+    attention's q/k/v projections.  x has 1..GEMV_MAX_ROWS rows; every pair
+    must pass ``linear_eligible``.  Each result equals ``linear_hip`` on its
+    linear bit for bit (same kernel)."""
+    biases = list(biases) if biases is not None else [None] * len(weights)
+    require_device(x, *weights, *[b for b in biases if b is not None])
+    if not 1 <= len(weights) <= 3 or len(biases) != len(weights):
+        raise ValueError("linear_multi_hip: one to three linears")
+    x2d = _gemm_ready(rows2d(x))
+    M, K = x2d.shape
+    if not 1 <= M <= GEMV_MAX_ROWS:
+        raise ValueError(f"linear_multi_hip: {M} rows (decode GEMV takes 1..{GEMV_MAX_ROWS})")
+    for w, b in zip(weights, biases):
+        if not linear_eligible(x, w, b):
+            raise ValueError(f"linear_multi_hip: unsupported shape x{tuple(x.shape)} "
+                             f"w{tuple(w.shape)}")
+    ws = [_gemm_ready(w) for w in weights]
+    bs = [None if b is None else b.contiguous() for b in biases]
+    outs = [torch.empty((M, w.shape[0]), dtype=x.dtype, device=x.device) for w in ws]
+    n = len(ws)
+    P, I64 = ctypes.c_void_p * n, ctypes.c_int64 * n
+    with _lib.device_of(x):
+        _lib.call("umic_linear_multi_bf16", x2d.data_ptr(), M, K, ld(x2d), n,
+                  P(*[w.data_ptr() for w in ws]), P(*[_lib.ptr(b) for b in bs]),
+                  P(*[o.data_ptr() for o in outs]), I64(*[w.shape[0] for w in ws]),
+                  I64(*[ld(w) for w in ws]), I64(*[w.shape[0] for w in ws]), 0,
+                  _lib.stream_of(x))
+    return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
 
 
 def stream_k_planned(x: torch.Tensor, weight: torch.Tensor) -> bool:
