@@ -269,6 +269,20 @@ int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int
                            void* stream);
 
 /*
+ * out = residual + (x @ w^T + bias) with the eager chain's two bf16
+ * roundings (the linear's output, then the sum): the decoder layer's MLP
+ * residual add folded into the down projection at decode.  M must be 1..8
+ * (the GEMV path; else UMIC_ERR_UNSUPPORTED; M == 0 is a no-op).  residual:
+ * [M, N] bf16, row stride ldr; out may alias residual only if ldr == ldo.
+ * Other rules as umic_linear_bf16.  No counterpart in the reference, whose
+ * decoder layer (transformers Qwen3VLTextDecoderLayer.forward) adds the MLP
+ * output to the residual stream in a separate op.
+ */
+int umic_linear_add_bf16(const void* x, const void* w, const void* bias, const void* residual,
+                         void* out, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                         int64_t ldr, int64_t ldo, void* stream);
+
+/*
  * Fused P5 MLP front half: out = silu(x @ wg^T) * (x @ wu^T), one bf16
  * rounding of the fp32 product.  wg, wu: [N, K] nn.Linear weights (the
  * reference passes them as .t() views; same memory).

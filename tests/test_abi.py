@@ -36,7 +36,7 @@ def test_header_declares_expected_entry_points():
     for n in ("umic_rmsnorm_bf16", "umic_add_rmsnorm_bf16", "umic_layernorm_bf16",
               "umic_add_layernorm_bf16", "umic_rope_qk_bf16", "umic_linear_bf16",
               "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
-              "umic_linear_multi_bf16",
+              "umic_linear_multi_bf16", "umic_linear_add_bf16",
               "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
               "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_version", "umic_error_string"):
         assert n in names
@@ -187,6 +187,17 @@ def test_linear_multi_rejection(lib):
     assert f(fake, 1, 128, 128, 3, w, None, out, N, I3(128, 64, 128), ldo, 0, None) == E_ARG
     assert f(fake, 1, 128, 128, 3, P3(fake, fake + 2, fake), None, out, N, ldw, ldo, 0,
              None) == E_UNS                                             # misaligned w
+
+
+def test_linear_add_rejection(lib):
+    E_ARG, E_UNS = -1, -2
+    f = lib.umic_linear_add_bf16
+    fake = 1 << 20
+    assert f(fake, fake, None, fake, fake, 0, 64, 128, 128, 128, 64, 64, None) == 0  # M = 0
+    assert f(fake, fake, None, fake, fake, 9, 64, 128, 128, 128, 64, 64, None) == E_UNS
+    assert f(fake, fake, None, None, fake, 1, 64, 128, 128, 128, 64, 64, None) == E_ARG
+    assert f(fake, fake, None, fake, fake, 1, 64, 128, 128, 128, 32, 64, None) == E_ARG  # ldr
+    assert f(fake, fake, None, fake, fake, 1, 64, 80, 128, 128, 64, 64, None) == E_UNS   # K % 32
 
 
 def test_wrappers_refuse_cpu_tensors():

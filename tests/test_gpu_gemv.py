@@ -157,3 +157,19 @@ def test_linear_multi_empty_segment_and_rows_bound():
     assert torch.equal(o0, linear.linear_hip(x, w0)) and torch.equal(o2, linear.linear_hip(x, w2))
     with pytest.raises(ValueError):
         linear.linear_multi_hip(bf16_randn(9, 256, gen=g).to(DEV), [w0])
+
+
+@pytest.mark.parametrize("M,with_bias", [(1, False), (4, True)])
+def test_linear_add_equals_linear_then_add(M, with_bias):
+    """umic_linear_add_bf16 = the eager chain residual + linear(x): the same
+    GEMV result rounded to bf16, then the bf16 sum, bit for bit."""
+    g = torch.Generator().manual_seed(120 + M)
+    N, K = 4096, 1536
+    x = bf16_randn(1, M, K, gen=g).to(DEV)
+    w = bf16_randn(N, K, scale=0.05, gen=g).to(DEV)
+    b = bf16_randn(N, scale=0.5, gen=g).to(DEV) if with_bias else None
+    r = bf16_randn(1, M, N, scale=4.0, gen=g).to(DEV)
+    out = linear.linear_add_hip(x, w, b, r)
+    ref = r + linear.linear_hip(x, w, b)
+    torch.cuda.synchronize()
+    assert out.shape == r.shape and torch.equal(out, ref)

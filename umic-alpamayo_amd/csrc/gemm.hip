@@ -69,6 +69,8 @@ struct GemmArgs {
   uint16_t* out;
   int64_t M, N, K, ldx, ldw0, ldw1, ldo;
   int tiles_m, tiles;
+  const uint16_t* resid;  // GEMV only: out = bf16(resid + bf16(result)), or NULL
+  int64_t ldr;
 };
 
 // LDS geometry of one operand tile of a K step: a row is BK bf16 = 64 bytes
@@ -828,7 +830,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g, GemvS
       const int64_t n = n0 + r;
       if (n >= g.N) continue;
       const float bias = BIAS && g.bias ? bf2f(g.bias[n]) : 0.0f;
-      const float o = gemv_epilogue<NB, ACT, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
+      float o = gemv_epilogue<NB, ACT, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
+      // the eager residual add after the linear: two bf16 roundings
+      if (g.resid) o = rbf(o) + bf2f(g.resid[m * g.ldr + n]);
       g.out[m * g.ldo + n] = (uint16_t)f2bf(o);
     }
   }
@@ -1083,4 +1087,23 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
                     : launch_gemv_segs<1, UMIC_ACT_GELU_TANH, false>(g, sg, st);
   return any_bias ? launch_gemv_segs<1, UMIC_ACT_NONE, true>(g, sg, st)
                   : launch_gemv_segs<1, UMIC_ACT_NONE, false>(g, sg, st);
+}
+
+extern "C" int umic_linear_add_bf16(const void* x, const void* w, const void* bias,
+                                    const void* residual, void* out, int64_t M, int64_t N,
+                                    int64_t K, int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldo,
+                                    void* stream) {
+  if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return UMIC_OK;
+  if (M > kGemvMaxRows) return UMIC_ERR_UNSUPPORTED;
+  if (!x || !w || !residual || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldw < K || ldr < N || ldo < N) return UMIC_ERR_INVALID_ARG;
+  if (K == 0) return UMIC_ERR_UNSUPPORTED;
+  if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
+  if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
+  GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
+             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0, (const uint16_t*)residual, ldr};
+  hipStream_t st = as_stream(stream);
+  return bias ? launch_gemv<1, UMIC_ACT_NONE, true>(g, st)
+              : launch_gemv<1, UMIC_ACT_NONE, false>(g, st);
 }

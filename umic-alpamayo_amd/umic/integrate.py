@@ -237,7 +237,8 @@ def _fused_residual_layer_forward(self, hidden_states, position_embeddings=None,
     """Decoder-layer forward with the attention-residual add fused into the
     post-attention RMSNorm: one kernel emits both the MLP input and the new
     residual stream.  The MLP residual add stays a plain add (its consumer is
-    the next layer's input norm).  Same call signature and return value as
+    the next layer's input norm), except at decode with the P5-fused MLP,
+    where it is the down projection's epilogue.  Same call signature and return value as
     the transformers decoder layer; extra keyword arguments pass through.
     """
     residual = hidden_states
@@ -247,8 +248,32 @@ def _fused_residual_layer_forward(self, hidden_states, position_embeddings=None,
         position_ids=position_ids, past_key_values=past_key_values,
         use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
     hidden_states, residual = _add_rmsnorm(self.post_attention_layernorm, hidden_states, residual)
+    out = _decode_mlp_residual(self.mlp, hidden_states, residual)
+    if out is not None:
+        return out
     hidden_states = self.mlp(hidden_states)
     return residual + hidden_states
+
+
+def _decode_mlp_residual(mlp: nn.Module, x: torch.Tensor, residual: torch.Tensor):
+    """residual + mlp(x) for a P5-fused MLP at decode (1..GEMV_MAX_ROWS rows):
+    the fused gate_silu_mul GEMV, then down_proj with the residual add in
+    its epilogue (umic_linear_add_bf16, the eager chain's two roundings).
+    None when the MLP is not the fused one or the call is not eligible."""
+    if getattr(mlp.forward, "__func__", None) is not _fused_mlp_forward:
+        return None
+    down = getattr(mlp, "down_proj", None)
+    wg, wu = mlp.gate_proj.weight, mlp.up_proj.weight
+    if not (isinstance(down, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS
+            and fused_ffn.p5_eligible(x, wg, wu)
+            and residual.dtype == x.dtype and residual.device == x.device
+            and residual.shape == (*x.shape[:-1], down.weight.shape[0])
+            and not grad_needed(x, residual, wg, wu, down.weight, down.bias)):
+        return None
+    h = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
+    if not linear.linear_eligible(h, down.weight, down.bias):
+        return residual + down(h)
+    return linear.linear_add_hip(h, down.weight, down.bias, residual)
 
 
 def fuse_add_rmsnorm(model: nn.Module, dry_run: bool = False) -> int:

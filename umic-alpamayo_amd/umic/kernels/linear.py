@@ -116,6 +116,34 @@ def linear_multi_hip(x: torch.Tensor, weights, biases=None) -> list[torch.Tensor
     return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
 
 
+def linear_add_hip(x: torch.Tensor, weight: torch.Tensor, bias, residual: torch.Tensor):
+    """residual + (x @ weight.T + bias), rounded as the eager chain rounds
+    (the linear's bf16 output, then the bf16 sum), in one decode-GEMV launch
+    (umic_linear_add_bf16).  x has 1..GEMV_MAX_ROWS rows; residual has the
+    output's shape."""
+    require_device(x, weight, residual, *([bias] if bias is not None else []))
+    if not linear_eligible(x, weight, bias):
+        raise ValueError(f"linear_add_hip: unsupported shape x{tuple(x.shape)} "
+                         f"w{tuple(weight.shape)}")
+    x2d = _gemm_ready(rows2d(x))
+    M, K = x2d.shape
+    N = weight.shape[0]
+    if not 1 <= M <= GEMV_MAX_ROWS:
+        raise ValueError(f"linear_add_hip: {M} rows (decode GEMV takes 1..{GEMV_MAX_ROWS})")
+    if residual.shape != (*x.shape[:-1], N) or residual.dtype != x.dtype:
+        raise ValueError(f"linear_add_hip: residual {tuple(residual.shape)} does not match "
+                         f"the output {(*x.shape[:-1], N)}")
+    w = _gemm_ready(weight)
+    b = None if bias is None else bias.contiguous()
+    r2d = rows2d(residual.contiguous())
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    with _lib.device_of(x):
+        _lib.call("umic_linear_add_bf16", x2d.data_ptr(), w.data_ptr(), _lib.ptr(b),
+                  r2d.data_ptr(), out.data_ptr(), M, N, K, ld(x2d), ld(w), N, N,
+                  _lib.stream_of(x))
+    return out.reshape(*x.shape[:-1], N)
+
+
 def stream_k_planned(x: torch.Tensor, weight: torch.Tensor) -> bool:
     """True if linear_hip(x, weight) runs the stream-K schedule on this device."""
     if not x.is_cuda:
