@@ -715,6 +715,7 @@ struct GemvSegs {
   int64_t N[kGemvMaxSegs], ldw[kGemvMaxSegs], ldo[kGemvMaxSegs];
   int64_t first[kGemvMaxSegs + 1];
   int count;
+  bool from_segs;  // the linears' operands come from here, not from GemmArgs
 };
 
 template <int NB, int ACT, bool BIAS, int MR>
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g, GemvS
 #pragma unroll
   for (int i = 1; i < kGemvMaxSegs; ++i)
     if (i < sg.count && (int64_t)blockIdx.x >= sg.first[i]) seg = i;
-  if (sg.count > 1) {
+  if (sg.from_segs) {
     g.w0 = g.w1 = sg.w[seg];
     g.bias = sg.bias[seg];
     g.out = sg.out[seg];
@@ -1056,6 +1057,7 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
   if (K == 0) return UMIC_ERR_UNSUPPORTED;
   GemvSegs sg{};
   sg.count = count;
+  sg.from_segs = true;
   bool any_bias = false;
   int64_t first = 0;
   for (int i = 0; i < count; ++i) {
