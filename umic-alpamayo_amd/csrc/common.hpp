@@ -105,19 +105,39 @@ __device__ __forceinline__ void st_stream(u32x4* p, const u32x4& v) {
 // Butterfly sum over aligned groups of G lanes (G a power of two <= 64);
 // every lane of the group ends with the group total.
 
-template <int G>
-__device__ __forceinline__ double group_sum(double v) {
+// Inside a 16-lane row the steps are DPP moves (full-rate VALU, no LDS
+// crossbar): quad_perm lane ^ 1 and ^ 2; after those every lane of a quad
+// holds the quad sum, so row_half_mirror (lane -> 7 - lane) and row_mirror
+// (lane -> 15 - lane) add the partner quad and half-row.  G = 32, 64 finish
+// with shuffles.  The result is the same sum combined in another order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+template <int G, typename T>
+__device__ __forceinline__ T group_sum_dpp(T v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G: a power of two up to 64");
+  if constexpr (G >= 2) v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp_move<0x141>(v);  // row_half_mirror
+  if constexpr (G >= 16) v += dpp_move<0x140>(v); // row_mirror
 #pragma unroll
-  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  for (int m = 16; m < G; m <<= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
 
 template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
+__device__ __forceinline__ double group_sum(double v) { return group_sum_dpp<G>(v); }
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) { return group_sum_dpp<G>(v); }
 
 // Correctly rounded fp32 1/sqrt(v): evaluated in double, rounded once.
 __device__ __forceinline__ float rsqrt_cr(float v) {

@@ -249,15 +249,6 @@ constexpr int kKvItems = 1;
 // sum would, the mean is rounded once to fp32 and the reciprocal square root
 // is correctly rounded -- the norm kernel's numerics.  Called with the whole
 // row active (rows are skipped or kept as a unit).
-// v from another lane of the same 16-lane row (DPP control CTRL), both
-// 32-bit halves moved with v_mov_dpp.
-template <int CTRL>
-__device__ __forceinline__ double dpp_move(double v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
-  return __hiloint2double(hi, lo);
-}
-
 __device__ __forceinline__ void rms_norm_chunks(float (&xl)[8], float (&xh)[8],
                                                 const u32x4 (&w)[2], int G, double inv_d,
                                                 float eps) {
