@@ -363,35 +363,6 @@ def copy_ceiling() -> int:
     return 0
 
 
-def hbm_ceiling() -> int:
-    """HBM streaming ceilings for the norm/RoPE access pattern: runs the
-    probe program built from csrc/probes/hbm_ceiling.hip (pure read, pure
-    write, and copies of the byte counts the norm kernels move) as a child
-    process and prints its JSON lines, then one summary line with the best
-    rate per pattern and size."""
-    import subprocess
-
-    exe = os.path.join(ROOT, "umic-alpamayo_amd", "umic", "lib", "hbm_ceiling")
-    if not os.path.exists(exe):
-        print(f"bench.py: {exe} is not built (run umic-alpamayo_amd/build.py)", file=sys.stderr)
-        return 1
-    proc = subprocess.run([exe], capture_output=True, text=True, timeout=240)
-    sys.stdout.write(proc.stdout)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stderr)
-        return proc.returncode
-    best: dict[str, dict] = {}
-    for line in proc.stdout.splitlines():
-        r = json.loads(line)
-        key = f"{r['pattern']}_{int(r['bytes_moved'])}"
-        if key not in best or r["tbps"] > best[key]["tbps"]:
-            best[key] = r
-    print(json.dumps({"hbm_ceiling_best": {k: {"us": v["us"], "tbps": v["tbps"],
-                                                "blocks_per_cu": v["blocks_per_cu"]}
-                                            for k, v in best.items()}}), flush=True)
-    return 0
-
-
 def _config5_layer():
     """BASELINE config 5 text decoder layer in bf16 on the GPU with random
     N(0, 0.02) weights (norms 1 + N(0, 0.1)), its rotary embedding and the
@@ -649,8 +620,6 @@ def main() -> int:
                     help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain device copies of the norm/RoPE byte counts")
-    ap.add_argument("--hbm-ceiling", action="store_true",
-                    help="HBM read / write / copy ceilings from the csrc/probes program")
     ap.add_argument("--vit-sites", action="store_true",
                     help="time the ViT projection sites, this library against hipBLASLt")
     ap.add_argument("--decode-layer", action="store_true",
@@ -671,8 +640,6 @@ def main() -> int:
         return pmc_probe()
     if args.copy_ceiling:
         return copy_ceiling()
-    if args.hbm_ceiling:
-        return hbm_ceiling()
     if args.vit_sites:
         return vit_sites()
     if args.decode_layer:

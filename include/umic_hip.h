@@ -157,10 +157,12 @@ int umic_rope_kv_append_bf16(const void* q, const void* k, const void* v,
  * then rotated as umic_rope_qk_bf16 in UMIC_ROPE_TEXT mode, in one launch:
  * q and k are read once and written once.  Same arguments as
  * umic_rope_qk_bf16 (TEXT mode, bf16 cos/sin) plus the two norm weights and
- * eps.  Requires D/16 to be a power of two up to 64 (D in 16..1024), every
- * stride a multiple of 8 elements and 16-byte aligned pointers, weights
- * included (else UMIC_ERR_UNSUPPORTED).  Results are bit-identical to
- * umic_rmsnorm_bf16 on each head row followed by umic_rope_qk_bf16.
+ * eps.  Requires D = 128 or 256 (head sizes whose eager q_norm / k_norm
+ * reduction order the kernel reproduces), every stride a multiple of 8
+ * elements and 16-byte aligned pointers, weights included (else
+ * UMIC_ERR_UNSUPPORTED).  Results are bit-identical to umic_rmsnorm_bf16 on
+ * the [B*S*Hq, D] q rows and [B*S*Hk, D] k rows followed by
+ * umic_rope_qk_bf16, and to the eager chain.
  * Replaces: the q_norm / k_norm forwards (integrate.py:134-141 on the
  * q_norm / k_norm modules of HF Qwen3VLTextAttention) followed by
  * kernels/rope.py:86-107 (make_text_rope) -- three launches.

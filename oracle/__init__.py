@@ -24,6 +24,11 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "liboracle.so")
 
+# gfx950 v_rcp_f32 / v_rsq_f32 as measured deltas from the correctly rounded
+# values (tests/golden/make_gfx950_tables.py); kept alive for the C side.
+HW_TABLES = os.path.join(os.path.dirname(_HERE), "tests", "golden", "gfx950_rcp_rsq.npz")
+_tables: list[np.ndarray] = []
+
 _lib = None
 
 
@@ -45,21 +50,35 @@ def _load():
             "orc_f32_to_bf16": [P, P, I64],
             "orc_bf16_to_f32": [P, P, I64],
             "orc_rmsnorm": [P, P, P, I64, I64, F32],
+            "orc_rms_var": [P, P, I64, I64],
             "orc_add_rmsnorm": [P, P, P, P, P, I64, I64, F32],
-            "orc_layernorm": [P, P, P, P, I64, I64, F32],
-            "orc_add_layernorm": [P, P, P, P, P, P, I64, I64, F32],
+            "orc_set_hw_tables": [P, I64, P],
+            "orc_layernorm": [P, P, P, P, P, P, I64, I64, F32, I],
+            "orc_add_layernorm": [P, P, P, P, P, P, I64, I64, F32, I],
             "orc_rope_text": [P, P, P, P, I64, I64, I64],
             "orc_rope_vision": [P, P, P, P, I64, I64, I64],
             "orc_gemm_nt_f32": [P, P, P, I64, I64, I64],
             "orc_gate_silu_mul": [P, P, P, P, I64, I64, I64, I],
             "orc_linear": [P, P, P, P, I64, I64, I64, I, I],
         }
+        ret = {"orc_rmsnorm", "orc_rms_var", "orc_add_rmsnorm", "orc_layernorm",
+               "orc_add_layernorm"}
         for name, args in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = None
+            fn.restype = ctypes.c_int if name in ret else None
+        with np.load(HW_TABLES, allow_pickle=False) as t:
+            _tables[:] = [np.ascontiguousarray(t["rcp_delta"], np.int8),
+                          np.ascontiguousarray(t["rsq_delta2"], np.uint8)]
+        lib.orc_set_hw_tables(_tables[0].ctypes.data_as(ctypes.c_void_p), _tables[0].size,
+                              _tables[1].ctypes.data_as(ctypes.c_void_p))
         _lib = lib
     return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise ValueError(f"oracle {what}: unsupported shape (code {rc})")
 
 
 def _p(a: np.ndarray | None):
@@ -92,35 +111,66 @@ def f32_from_bf16(a: np.ndarray) -> np.ndarray:
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """HF Qwen3VLTextRMSNorm over the last dim, in torch-ROCm's reduction
+    order for a [rows, n] input (rows = every leading dim)."""
     x, w = _u16(x), _u16(w)
     n = x.shape[-1]
     y = np.empty_like(x)
-    _load().orc_rmsnorm(_p(x), _p(w), _p(y), x.size // n, n, eps)
+    _check(_load().orc_rmsnorm(_p(x), _p(w), _p(y), x.size // n, n, eps), "rmsnorm")
     return y
+
+
+def rms_var(x: np.ndarray) -> np.ndarray:
+    """torch-ROCm's fp32 x.float().pow(2).mean(-1) of [rows, n] bf16 bits."""
+    x = _u16(x)
+    n = x.shape[-1]
+    var = np.empty(x.size // n, np.float32)
+    _check(_load().orc_rms_var(_p(x), _p(var), x.size // n, n), "rms_var")
+    return var
 
 
 def add_rmsnorm(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float):
     x, r, w = _u16(x), _u16(r), _u16(w)
     n = x.shape[-1]
     normed, summed = np.empty_like(x), np.empty_like(x)
-    _load().orc_add_rmsnorm(_p(x), _p(r), _p(w), _p(normed), _p(summed), x.size // n, n, eps)
+    _check(_load().orc_add_rmsnorm(_p(x), _p(r), _p(w), _p(normed), _p(summed), x.size // n,
+                                   n, eps), "add_rmsnorm")
     return normed, summed
 
 
-def layernorm(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+def layernorm_torch_order(n: int, aligned: bool = True) -> bool:
+    """Whether eager's layer_norm takes its vectorized kernel (the restated
+    Welford order): n % 4 == 0 and an 8-byte aligned contiguous input."""
+    return n % 4 == 0 and aligned
+
+
+def layernorm(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float,
+              aligned: bool = True, stats: bool = False, _cr_recip: bool = False):
+    """torch layer_norm of bf16 rows; with stats=True also (mean, rstd).
+    ``_cr_recip`` (tests only) plants a mistake: the torch order with
+    correctly rounded reciprocals instead of gfx950's v_rcp_f32 / v_rsq_f32."""
     x, w, b = _u16(x), _u16(w), _u16(b)
     n = x.shape[-1]
+    rows = x.size // n
     y = np.empty_like(x)
-    _load().orc_layernorm(_p(x), _p(w), _p(b), _p(y), x.size // n, n, eps)
-    return y
+    mean, rstd = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    order = int(layernorm_torch_order(n, aligned))
+    if order and _cr_recip:
+        order = 2
+    _check(_load().orc_layernorm(_p(x), _p(w), _p(b), _p(y), _p(mean), _p(rstd), rows, n, eps,
+                                 order), "layernorm")
+    return (y, mean, rstd) if stats else y
 
 
 def add_layernorm(x, r, w, b, eps: float):
+    """bf16(x + r), then layer_norm of the rounded sum (a fresh, aligned
+    tensor in eager, so the vectorized kernel's order whenever n % 4 == 0)."""
     x, r, w, b = _u16(x), _u16(r), _u16(w), _u16(b)
     n = x.shape[-1]
     normed, summed = np.empty_like(x), np.empty_like(x)
-    _load().orc_add_layernorm(_p(x), _p(r), _p(w), _p(b), _p(normed), _p(summed),
-                              x.size // n, n, eps)
+    _check(_load().orc_add_layernorm(_p(x), _p(r), _p(w), _p(b), _p(normed), _p(summed),
+                                     x.size // n, n, eps, int(layernorm_torch_order(n))),
+           "add_layernorm")
     return normed, summed
 
 

@@ -30,6 +30,22 @@ def ulp_hist(d: np.ndarray, cap: int = 4) -> dict:
     return {f"{i}": int((d == i).sum()) for i in range(cap)} | {f">={cap}": int((d >= cap).sum())}
 
 
+def log_parity(op: str, shape, d: np.ndarray, against: str = "torch eager (GPU)") -> dict:
+    """Record a bf16 ulp histogram of a kernel against eager: printed, and
+    appended as a JSON line to the file named by $UMIC_PARITY_LOG if set."""
+    import json
+    import os
+
+    rec = {"op": op, "shape": list(shape), "against": against, "elements": int(d.size),
+           "max_ulp": int(d.max()) if d.size else 0, "hist": ulp_hist(d)}
+    print(f"parity {op} {tuple(shape)} vs {against}: {rec['hist']}", flush=True)
+    path = os.environ.get("UMIC_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    return rec
+
+
 def bf16_randn(*shape, scale=1.0, shift=0.0, gen=None) -> torch.Tensor:
     """N(shift, scale^2) drawn on the CPU in fp32, then rounded to bf16."""
     return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16)

@@ -13,7 +13,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
-from helpers import bf16_randn, bits
+from helpers import bf16_randn, bits, log_parity, ulp
 
 import oracle
 from umic.kernels import rope
@@ -63,6 +63,10 @@ def test_text_rope_hf_layout(S, Hq, Hk, D):
     assert np.array_equal(bits(ko.transpose(1, 2))[0], oracle.rope_text(bits(ks)[0], bits(cos)[0],
                                                                         bits(sin)[0]))
     rq, rk = apply_rotary_pos_emb(q, k, cos.to(DEV), sin.to(DEV))
+    for name, got, ref in (("q", qo, rq), ("k", ko, rk)):
+        d = ulp(bits(got), bits(ref))
+        log_parity(f"text_rope ({name})", tuple(ref.shape), d)
+        assert d.max() <= 1
     assert torch.equal(qo, rq) and torch.equal(ko, rk)
 
 
@@ -124,6 +128,10 @@ def test_vision_rope_packed_qkv(grid, H):
     assert np.array_equal(bits(qo), oracle.rope_vision(bits(qc), cos.numpy(), sin.numpy()))
     assert np.array_equal(bits(ko), oracle.rope_vision(bits(kc), cos.numpy(), sin.numpy()))
     rq, rk = apply_rotary_pos_emb_vision(q, k, cos.to(DEV), sin.to(DEV))
+    for name, got, ref in (("q", qo, rq), ("k", ko, rk)):
+        d = ulp(bits(got), bits(ref))
+        log_parity(f"vision_rope ({name})", tuple(ref.shape), d)
+        assert d.max() <= 1
     assert torch.equal(qo, rq) and torch.equal(ko, rk)
 
 

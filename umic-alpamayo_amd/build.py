@@ -7,8 +7,6 @@ Each csrc/*.hip file compiles to its own object under _build/ (in parallel),
 then all objects link into umic/lib/libumic_hip.so, the in-tree library the
 umic package loads.  Flags: -O3, gfx950 only, no fp contraction (every fp32
 rounding step in the kernels is explicit), and packed-fp32 codegen disabled.
-csrc/probes/hbm_ceiling.hip, a measurement program (not part of the
-library), builds into umic/lib/hbm_ceiling for ``bench.py --hbm-ceiling``.
 """
 
 from __future__ import annotations
@@ -76,25 +74,7 @@ def build(force: bool = False, jobs: int | None = None) -> str:
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
-    _build_probe(force)
     return LIB
-
-
-PROBE_SRC = os.path.join(CSRC, "probes", "hbm_ceiling.hip")
-PROBE = os.path.join(LIB_DIR, "hbm_ceiling")
-
-
-def _build_probe(force: bool) -> None:
-    """The HBM streaming-ceiling program used by bench.py --hbm-ceiling."""
-    if not force and os.path.exists(PROBE) and os.path.getmtime(PROBE) >= os.path.getmtime(PROBE_SRC):
-        return
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", PROBE_SRC, "-o",
-           PROBE + ".tmp"]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError("hipcc failed for hbm_ceiling.hip:\n" + proc.stderr)
-    os.replace(PROBE + ".tmp", PROBE)
 
 
 if __name__ == "__main__":

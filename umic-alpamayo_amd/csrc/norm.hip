@@ -1,25 +1,48 @@
 // Row normalisation kernels for gfx950: RMSNorm, residual-add + RMSNorm,
 // LayerNorm (affine, bias) and residual-add + LayerNorm, all bf16 in/out.
 //
-// HBM-bound design: every element is read once and written once.  A row is
-// owned by an aligned group of LPR lanes of one wavefront; each lane holds
-// up to MAXV 16-byte vectors of the row in registers (lane-interleaved, so
-// every load/store instruction of the group covers LPR*16 contiguous bytes).
-// Row statistics are reduced with cross-lane butterflies only -- no LDS, no
-// barriers -- and the normalised values are written straight from the
-// registers the row was loaded into.  Rows that fit neither the 16-byte
-// vector layout nor 16*64*8 elements take a block-per-row generic kernel.
+// Numerics: eager's, bit for bit.  The eager modules these kernels replace
+// (HF Qwen3VLTextRMSNorm, torch layer_norm) take their row statistics on
+// the GPU in fp32, in an order fixed by torch's own kernels, and a
+// statistic one fp32 ulp away from eager's moves a bf16 output by up to two
+// ulps.  So every kernel here reproduces torch-ROCm's order exactly:
 //
-// Numerics.  Row statistics come from exact double sums of x and x^2 (a
-// bf16 square is exact in fp32; the double sums of bf16-derived terms are
-// exact for activation-range data, hence independent of summation order):
-// mean = sum/n and var = sumsq/n - mean^2 in double, each rounded once to
-// fp32, rstd = 1/sqrt(var + eps) in double rounded once.  Every bf16
-// rounding point of the eager op chain is kept:
-//   RMSNorm     y = bf16(w * bf16(x * rstd))          (HF Qwen3VLTextRMSNorm)
-//   LayerNorm   y = bf16(fma(w, rstd * (x - mean), b)) (torch layer_norm)
-//   add+norm    s = bf16(x + r), then the norm of the ROUNDED s (eager adds
-//               the residual as its own bf16 op before the norm).
+//   RMSNorm   mean(x^2) is aten's generic reduction (ATen/native/hip/
+//             Reduce.cuh): setReduceConfig picks, from [rows, n], the
+//             threads across a row (bw), whether each thread reads 4-element
+//             vectors, and whether a row is also split over wavefronts;
+//             each thread keeps 4 accumulators, combines them in order, and
+//             the threads combine in a fixed tree (a shared-memory halving
+//             down to 64, then shuffles with offsets 1, 2, 4, ... on ROCm).
+//             The mean is sum * (rows / (rows * n)); rsqrt is correctly
+//             rounded (torch.rsqrt on this platform).
+//   LayerNorm aten's vectorized_layer_norm_kernel (64x4 threads): thread t
+//             runs Welford over the 4-element vectors t, t + 256, ...; the
+//             wavefronts combine with shuffle-down offsets 32 .. 1, then
+//             across the four wavefronts; count reciprocals are v_rcp_f32,
+//             rstd is v_rsq_f32(m2 / n + eps), and the fused products are
+//             the ones the ROCm build contracts.  Rows torch sends to its
+//             other LayerNorm kernel (n % 4 != 0, a contiguous input off
+//             8-byte alignment) take exact statistics here instead.
+//
+// Layouts.  The register paths keep each row in registers, so a row is read
+// once and written once:
+//   RMSNorm   a group of bw/2 lanes owns a row; lane l holds the vectors
+//             l, l + bw/2, ... -- exactly the data of torch's reducing
+//             threads 2l and 2l + 1, so the per-thread sums are formed in
+//             place and the tree is the pair, then a lane butterfly.
+//   LayerNorm 16 lanes own a row; lane l holds torch's threads l + 16k of
+//             each wavefront (4-element vectors), so the first two steps of
+//             torch's shuffle tree and its cross-wavefront tree run in-lane
+//             and the rest is a 16-lane butterfly with the tree's (own,
+//             other) orientation kept.
+// Every other shape takes a block-per-row kernel that runs the same
+// reduction with one hardware thread per torch thread.
+//
+// Eager's bf16 rounding points are kept:
+//   RMSNorm     y = bf16(w * bf16(x * rstd))            (HF Qwen3VLTextRMSNorm)
+//   LayerNorm   y = bf16(fma(w, rstd * (x - mean), b))  (torch layer_norm)
+//   add+norm    s = bf16(x + r), then the norm of the ROUNDED s.
 #include "common.hpp"
 
 namespace umic {
@@ -39,16 +62,110 @@ struct NormArgs {
   uint16_t* s;        // summed output (add ops)
   int64_t rows, n, ldx, ldr, ldy, lds;
   float eps;
+  float factor;  // RMSNorm: aten MeanOps factor, float(rows) / float(rows * n)
 };
 
-// ---- register-resident fast path -----------------------------------------
+// ---- torch's reduction plan for the RMSNorm statistic (host side) --------
 
-// RPG rows per group: rows of one or two vectors per lane (e.g. the
-// [S*H, 128] per-head q/k norms) leave a wavefront only 1-2 KB of loads in
-// flight, too little to cover HBM latency; a group then takes RPG
-// consecutive rows and issues all their loads before reducing any.
-template <int OP, int LPR, int MAXV, int RPG>
-__global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, int vpl) {
+// setReduceConfig (Reduce.cuh) for a contiguous fp32 [rows, n] tensor reduced
+// over its last dim on a 64-lane, 512-threads-per-block device: vec = the
+// threads read 4-element vectors (n >= 128), bw threads across a row, bh the
+// block height, split = the row is also divided over the bh wavefronts.
+struct RmsPlan {
+  int vec, bw, bh, split;
+};
+
+inline int last_pow2(int64_t v) {
+  int p = 1;
+  while ((int64_t)p * 2 <= v) p *= 2;
+  return p;
+}
+
+// false when torch would also split rows across blocks (n >= 131072)
+inline bool rms_plan(int64_t rows, int64_t n, RmsPlan& p) {
+  constexpr int kMaxThreads = 512;
+  int64_t dim0 = n;
+  p.vec = dim0 >= 128;
+  if (p.vec) dim0 /= 4;
+  const int d0 = dim0 < kMaxThreads ? last_pow2(dim0) : kMaxThreads;
+  const int d1 = rows < kMaxThreads ? last_pow2(rows) : kMaxThreads;
+  int bw = d0 < kWave ? d0 : kWave;
+  const int bh = d1 < kMaxThreads / bw ? d1 : kMaxThreads / bw;
+  bw = d0 < kMaxThreads / bh ? d0 : kMaxThreads / bh;
+  const int64_t vpt = (n + bw - 1) / bw;
+  p.bw = bw;
+  p.bh = bh;
+  p.split = vpt >= (bh * 16 < 256 ? bh * 16 : 256);
+  return !(p.split && (n + (int64_t)bw * bh - 1) / ((int64_t)bw * bh) >= 256);
+}
+
+// ---- LayerNorm Welford pieces (torch-ROCm's arithmetic) -------------------
+
+struct Wf {
+  float mean, m2, n;
+};
+
+// v_rcp_f32 of a count.  The empty asm keeps the count opaque: in the
+// unrolled register path the counts are compile-time constants (every
+// Welford state starts at 0), and the compiler folds the instruction on a
+// constant to the correctly rounded 1/c -- which differs from the hardware
+// result on ~10% of counts, and eager runs the instruction.
+__device__ __forceinline__ float hw_rcp(float c) {
+  asm volatile("" : "+v"(c));
+  return __builtin_amdgcn_rcpf(c);
+}
+
+// One element: the mean update fused with the hardware count reciprocal,
+// the m2 update as two roundings (cuWelfordOnlineSum as the ROCm build
+// compiles it).
+__device__ __forceinline__ Wf wf_push(Wf a, float v) {
+  const float delta = v - a.mean;
+  const float cnt = a.n + 1.0f;
+  const float mean = __builtin_fmaf(delta, hw_rcp(cnt), a.mean);
+  const float m2 = a.m2 + delta * (v - mean);
+  return Wf{mean, m2, cnt};
+}
+
+// cuWelfordCombine(b = own, a = other).  INTRA: the wavefront tree contracts
+// the mean as fma(nA, meanA, nB * meanB); the cross-wavefront tree as
+// fma(nB, meanB, nA * meanA).  m2 takes fma(delta^2 * countA, nB, m2A + m2B).
+template <bool INTRA>
+__device__ __forceinline__ Wf wf_combine(Wf b, Wf a) {
+  const float delta = b.mean - a.mean;
+  const float cnt = a.n + b.n;
+  if (!(cnt > 0.0f)) return Wf{0.0f, 0.0f, cnt};
+  const float coef = hw_rcp(cnt);
+  const float na = a.n * coef, nb = b.n * coef;
+  const float mean = INTRA ? __builtin_fmaf(na, a.mean, nb * b.mean)
+                           : __builtin_fmaf(nb, b.mean, na * a.mean);
+  const float m2 = __builtin_fmaf((delta * delta) * a.n, nb, a.m2 + b.m2);
+  return Wf{mean, m2, cnt};
+}
+
+// The partner lane (lane ^ K, K <= 16) through ds_swizzle's bitmask mode.
+template <int K>
+__device__ __forceinline__ float swz_xor(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (K << 10) | 0x1F));
+}
+
+// One butterfly step of the wavefront tree over lane bit K: both lanes of a
+// pair compute combine(lower lane's state, upper lane's state).
+template <int K>
+__device__ __forceinline__ Wf wf_step(Wf s, bool upper) {
+  const Wf o{swz_xor<K>(s.mean), swz_xor<K>(s.m2), swz_xor<K>(s.n)};
+  return upper ? wf_combine<true>(o, s) : wf_combine<true>(s, o);
+}
+
+// ---- register path: RMSNorm ----------------------------------------------
+
+// LPR = bw/2 lanes own a row; lane l holds the 16-byte vectors l + LPR*j,
+// the data of torch's reducing threads 2l (elements 0..3 of each vector) and
+// 2l + 1 (elements 4..7).  RPG rows per group: rows of one or two vectors per
+// lane (e.g. the [S*H, 128] per-head q/k norms) leave a wavefront only 1-2 KB
+// of loads in flight, too little to cover HBM latency; a group then takes
+// RPG consecutive rows and issues all their loads before reducing any.
+template <bool ADD, int LPR, int MAXV, int RPG>
+__global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int vpl) {
   const int rows_per_block = (int)blockDim.x / LPR * RPG;
   const int lane = threadIdx.x & (LPR - 1);
   const int64_t row0 = (int64_t)blockIdx.x * rows_per_block + (threadIdx.x / LPR) * RPG;
@@ -56,12 +173,10 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, in
   // the butterflies below only ever read lanes of a live group.
   if (row0 >= a.rows) return;
 
-  // The rows' source values stay packed as bf16 (16 B per 8 elements) in
-  // registers between the statistics pass and the output pass.  Loads are
-  // issued unconditionally (a dead slot re-reads vector 0, a row past the
-  // end re-reads row0; both are zeroed or never stored): predicated loads
-  // would sit in branches, and every branch join costs a full vmcnt drain
-  // -- the loads must all be in flight together.
+  // Loads are issued unconditionally (a dead slot re-reads vector 0, a row
+  // past the end re-reads row0; both are zeroed or never stored): predicated
+  // loads would sit in branches, and every branch join costs a full vmcnt
+  // drain -- the loads must all be in flight together.
   const u32x4 zero = {0u, 0u, 0u, 0u};
   bool live[MAXV];
   int cix[MAXV];
@@ -85,7 +200,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, in
 #pragma unroll
     for (int i = 0; i < MAXV; ++i) sv[r][i] = ld_stream(xp + cix[i]);
   }
-  if constexpr (has_add(OP)) {
+  if constexpr (ADD) {
     u32x4 rv[RPG][MAXV];
 #pragma unroll
     for (int r = 0; r < RPG; ++r) {
@@ -112,74 +227,333 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a, int nvec, in
   }
 
   const u32x4* wp = reinterpret_cast<const u32x4*>(a.w);
-  const u32x4* bp = reinterpret_cast<const u32x4*>(a.b);
-  u32x4 wv[MAXV], bv[MAXV];
-  const double inv_n = 1.0 / (double)a.n;
+  u32x4 wv[MAXV];
 #pragma unroll
   for (int r = 0; r < RPG; ++r) {
-#pragma unroll
-    for (int i = 0; i < MAXV; ++i) sv[r][i] = live[i] ? sv[r][i] : zero;
-
-    // Exact double sums (zero-filled tail vectors contribute nothing).  Four
-    // independent accumulators keep the f64 add chains short; the sums are
-    // exact, so the grouping does not change them.
-    double sum4[4] = {0.0, 0.0, 0.0, 0.0}, ssq4[4] = {0.0, 0.0, 0.0, 0.0};
+    // torch's per-thread sums: thread 2l keeps acc[0..3] over elements 0..3 of
+    // its vectors, thread 2l + 1 acc[4..7] over elements 4..7, in vector order
+    // (a dead slot adds +0, which changes nothing).
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < MAXV; ++i) {
+      if (!live[i]) sv[r][i] = zero;
       float f[8];
       unpack8(sv[r][i], f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if constexpr (is_ln(OP)) sum4[e & 3] += (double)f[e];
-        ssq4[e & 3] += (double)(f[e] * f[e]);  // a bf16 square is exact in fp32
-      }
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] + f[e] * f[e];
     }
-    double sum = (sum4[0] + sum4[1]) + (sum4[2] + sum4[3]);
-    double ssq = (ssq4[0] + ssq4[1]) + (ssq4[2] + ssq4[3]);
-    float rstd, mean = 0.f;
-    if constexpr (is_ln(OP)) {
-      sum = group_sum<LPR>(sum);
-      ssq = group_sum<LPR>(ssq);
-      const double mean_d = sum * inv_n;
-      mean = (float)mean_d;
-      rstd = rsqrt_cr((float)(ssq * inv_n - mean_d * mean_d) + a.eps);
-    } else {
-      rstd = rsqrt_cr((float)(group_sum<LPR>(ssq) * inv_n) + a.eps);
-    }
+    const float t_even = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    const float t_odd = ((acc[4] + acc[5]) + acc[6]) + acc[7];
+    // the shuffle tree over bw threads: the adjacent pair, then lane pairs
+    const float ssq = group_sum<LPR>(t_even + t_odd);
+    const float rstd = rsqrt_cr(ssq * a.factor + a.eps);
     if (r == 0) {
-      // weights (and bias), L2-resident, loaded once the first row's
-      // statistics are done: issued with the row loads they measured slower
+      // weights, L2-resident, loaded once the first row's statistic is
+      // done: issued with the row loads they measured slower
 #pragma unroll
-      for (int i = 0; i < MAXV; ++i) {
-        wv[i] = wp[cix[i]];
-        if constexpr (is_ln(OP)) bv[i] = bp[cix[i]];
-      }
+      for (int i = 0; i < MAXV; ++i) wv[i] = wp[cix[i]];
     }
 
     u32x4* yp = reinterpret_cast<u32x4*>(a.y + rows[r] * a.ldy);
 #pragma unroll
     for (int i = 0; i < MAXV; ++i) {
       if (!live[i] || !rlive[r]) continue;
-      const int c = cix[i];
       float f[8], wf[8], o[8];
       unpack8(sv[r][i], f);
       unpack8(wv[i], wf);
-      if constexpr (is_ln(OP)) {
-        float bf[8];
-        unpack8(bv[i], bf);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(wf[e], rstd * (f[e] - mean), bf[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
-      }
-      st_stream(yp + c, pack8(o));
+      for (int e = 0; e < 8; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+      st_stream(yp + cix[i], pack8(o));
     }
   }
 }
 
-// ---- generic path: one 256-thread block per row, scalar elements ---------
+// ---- register path: LayerNorm --------------------------------------------
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Word 3 of a raw buffer resource (the one gemm.hip uses): untyped dword
+// access with range checking against num_records.
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ void unpack4(const u32x2& v, float f[4]) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+}
+
+__device__ __forceinline__ u32x2 pack4(const float f[4]) {
+  u32x2 v;
+  v.x = pack2(f[0], f[1]);
+  v.y = pack2(f[2], f[3]);
+  return v;
+}
+
+// Sixteen lanes per row.  Torch's thread t = 64w + x (wavefront w, lane x)
+// reads the 4-element vectors t, t + 256, ...; here lane l of a row's group
+// holds the threads x = l + 16k, k = 0..3, of every wavefront w, so torch's
+// first two shuffle steps (offsets 32 and 16: bit 1 and bit 0 of k) run
+// in-lane, the next four (offsets 8 .. 1) are a lane butterfly over the 16
+// lanes, and the cross-wavefront tree (w with w + 2, then 0 with 1) is
+// in-lane again -- about 31 combines per lane and row.  Vector t + 256j of
+// thread (w, l + 16k) is element group 16m + l with m = 4w + k + 16j: slot m
+// of lane l, the slots below 4 * M4 = 4 * ceil(n / 256) held in registers.
+// Loads and stores are 8-byte chunks, 128 contiguous bytes per group, through
+// buffer resources over the wavefront's four rows.  The pushes take their
+// count reciprocals from a table of v_rcp_f32 results.
+template <bool ADD, int M4>
+__global__ __launch_bounds__(256) void ln_rows_kernel(NormArgs a, int nvec4) {
+  constexpr int G = 16, M = 4 * M4, kRowsPerWave = kWave / G;
+  constexpr int kNt = 2;  // buffer access cache policy: non-temporal (streamed once)
+  const int l = threadIdx.x & (G - 1);
+  // the wavefront's first row (uniform) and this group's row within its four
+  const int64_t wrow0 = __builtin_amdgcn_readfirstlane(
+      (int)((int64_t)blockIdx.x * (blockDim.x / G) + (threadIdx.x / kWave) * kRowsPerWave));
+  const int rw = (threadIdx.x & (kWave - 1)) / G;
+  const int64_t row = wrow0 + rw;
+  if (row >= a.rows) return;  // a group exits as a whole: its butterflies stay in it
+  const int64_t wrows = a.rows - wrow0 < kRowsPerWave ? a.rows - wrow0 : kRowsPerWave;
+
+  // Buffer resources over the wavefront's rows (uniform, so every access is
+  // one instruction): a slot past its row's end reads the gap or the next row
+  // (never pushed) or, past the last row, zeros; stores check the slot.
+  auto span = [&](const uint16_t* base, int64_t ld) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + wrow0 * ld), (short)0,
+                                             (int)(((wrows - 1) * ld + a.n) * 2), kRsrcWord3);
+  };
+  const int lx = (int)(rw * a.ldx * 2) + l * 8;  // byte offset of slot 0; slot m adds 128 m
+  const __amdgpu_buffer_rsrc_t xr = span(a.x, a.ldx);
+  u32x2 xv[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xv[m] = __builtin_amdgcn_raw_buffer_load_b64(xr, lx + 128 * m, 0, kNt);
+  if constexpr (ADD) {
+    const __amdgpu_buffer_rsrc_t rr = span(a.r, a.ldr);
+    const __amdgpu_buffer_rsrc_t sr = span(a.s, a.lds);
+    const int lr = (int)(rw * a.ldr * 2) + l * 8, ls = (int)(rw * a.lds * 2) + l * 8;
+    u32x2 rv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) rv[m] = __builtin_amdgcn_raw_buffer_load_b64(rr, lr + 128 * m, 0, kNt);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float xf[4], rf[4];
+      unpack4(xv[m], xf);
+      unpack4(rv[m], rf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xf[e] = xf[e] + rf[e];
+      xv[m] = pack4(xf);  // bf16(x + r): the eager residual add
+      if (16 * m + l < nvec4) __builtin_amdgcn_raw_buffer_store_b64(xv[m], sr, ls + 128 * m, 0, kNt);
+    }
+  }
+
+  // v_rcp_f32 of the counts a thread's pushes reach (at most 4 per 16 slots)
+  constexpr int kMaxCount = 4 * ((M + 15) / 16);
+  float rc[kMaxCount];
+#pragma unroll
+  for (int c = 0; c < kMaxCount; ++c) rc[c] = hw_rcp((float)(c + 1));
+
+  Wf wv[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    Wf st[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      Wf t{0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; 4 * w + k + 16 * j < M; ++j) {
+        const int m = 4 * w + k + 16 * j;
+        if (16 * m + l >= nvec4) break;  // a thread's vectors are a prefix of j
+        float f[4];
+        unpack4(xv[m], f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float delta = f[e] - t.mean;
+          t.mean = __builtin_fmaf(delta, rc[4 * j + e], t.mean);
+          t.m2 = t.m2 + delta * (f[e] - t.mean);
+        }
+        t.n = (float)(4 * (j + 1));
+      }
+      st[k] = t;
+    }
+    // torch offsets 32 and 16 (k bit 1, then bit 0), own state first
+    st[0] = wf_combine<true>(st[0], st[2]);
+    st[1] = wf_combine<true>(st[1], st[3]);
+    Wf sw = wf_combine<true>(st[0], st[1]);
+    // offsets 8, 4, 2, 1: the lane bits
+    sw = wf_step<8>(sw, l & 8);
+    sw = wf_step<4>(sw, l & 4);
+    sw = wf_step<2>(sw, l & 2);
+    sw = wf_step<1>(sw, l & 1);
+    wv[w] = sw;
+  }
+  // the cross-wavefront tree: w with w + 2, then 0 with 1
+  const Wf t = wf_combine<false>(wf_combine<false>(wv[0], wv[2]),
+                                 wf_combine<false>(wv[1], wv[3]));
+  const float mean = t.mean;
+  const float rstd = __builtin_amdgcn_rsqf(t.m2 / (float)a.n + a.eps);
+
+  const int w_bytes = (int)(a.n * 2);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t br =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.b, (short)0, w_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t yr = span(a.y, a.ldy);
+  const int ly = (int)(rw * a.ldy * 2) + l * 8;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (16 * m + l >= nvec4) continue;
+    float f[4], wf[4], bf[4], o[4];
+    unpack4(xv[m], f);
+    unpack4(__builtin_amdgcn_raw_buffer_load_b64(wr, l * 8 + 128 * m, 0, 0), wf);
+    unpack4(__builtin_amdgcn_raw_buffer_load_b64(br, l * 8 + 128 * m, 0, 0), bf);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(wf[e], rstd * (f[e] - mean), bf[e]);
+    __builtin_amdgcn_raw_buffer_store_b64(pack4(o), yr, ly + 128 * m, 0, kNt);
+  }
+}
+
+// ---- block-per-row paths -------------------------------------------------
+
+// Element j of the row the statistics are taken over: x, or bf16(x + r).
+// Recomputed on every pass (cheap, identical result) rather than re-read
+// from the summed output.
+template <bool ADD>
+__device__ __forceinline__ float src_val(const NormArgs& a, int64_t row, int64_t j) {
+  const float xf = bf2f(a.x[row * a.ldx + j]);
+  if constexpr (ADD) return rbf(xf + bf2f(a.r[row * a.ldr + j]));
+  return xf;
+}
+
+template <bool ADD>
+__device__ __forceinline__ float sq(const NormArgs& a, int64_t row, int64_t j) {
+  const float f = src_val<ADD>(a, row, j);
+  return f * f;
+}
+
+template <bool ADD>
+__device__ void write_sum(const NormArgs& a, int64_t row) {
+  if constexpr (ADD) {
+    uint16_t* sr = a.s + row * a.lds;
+    for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x)
+      sr[j] = (uint16_t)f2bf(src_val<ADD>(a, row, j));
+  }
+}
+
+// RMSNorm with torch's reduction for any plan: one hardware thread per
+// reducing thread (x = lane across the row, y = wavefront when the row is
+// split), the per-thread loops of Reduce.cuh's vectorized (with the head
+// and tail of a row off 16-byte alignment in the fp32 copy eager reduces:
+// row r starts (r * n) % 4 elements past it) and scalar forms, then
+// block_x_reduce and block_y_reduce through LDS.
+template <bool ADD>
+__global__ __launch_bounds__(512) void rms_block_kernel(NormArgs a, RmsPlan p) {
+  __shared__ float red[512];
+  __shared__ float yred[16];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int x = tid % p.bw, y = tid / p.bw;
+  write_sum<ADD>(a, row);
+  const int64_t n = a.n;
+  const int64_t step = (int64_t)p.bw * (p.split ? p.bh : 1);
+  const int64_t idx0 = x + (int64_t)(p.split ? y : 0) * p.bw;
+  const bool tail_ok = !p.split || y == 0;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.vec) {
+    const int shift = (int)((row * n) % 4);
+    int64_t j0 = 0, end = n;  // row elements j0 + [0, end) are vector-aligned
+    if (shift > 0) {
+      if (x >= shift && x < 4 && tail_ok) acc[0] = sq<ADD>(a, row, x - shift);
+      j0 = 4 - shift;
+      end = n - j0;
+    }
+    for (int64_t idx = idx0; idx * 4 + 3 < end; idx += step) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + sq<ADD>(a, row, j0 + idx * 4 + i);
+    }
+    const int64_t tail = end - end % 4;
+    if (tail_ok && tail + x < end) acc[0] = acc[0] + sq<ADD>(a, row, j0 + tail + x);
+  } else {
+    int64_t idx = idx0;
+    for (; idx + 3 * step < n; idx += 4 * step) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + sq<ADD>(a, row, idx + i * step);
+    }
+    for (int i = 0; i < 4 && idx < n; ++i, idx += step) acc[i] = acc[i] + sq<ADD>(a, row, idx);
+  }
+  red[tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  __syncthreads();
+  for (int off = p.bw / 2; off >= kWave; off >>= 1) {  // shared-memory halving
+    if (x < off) red[tid] = red[tid] + red[tid + off];
+    __syncthreads();
+  }
+  const int w = p.bw < kWave ? p.bw : kWave;
+  for (int off = 1; off < w; off <<= 1) {  // the shuffle tree, offsets upward
+    if (x % (2 * off) == 0 && x + off < w) red[tid] = red[tid] + red[tid + off];
+    __syncthreads();
+  }
+  float total = red[0];
+  if (p.split) {
+    if (x == 0) yred[y] = red[tid];
+    __syncthreads();
+    for (int off = p.bh / 2; off > 0; off >>= 1) {  // block_y_reduce
+      if (tid < off) yred[tid] = yred[tid] + yred[tid + off];
+      __syncthreads();
+    }
+    total = yred[0];
+  }
+  const float rstd = rsqrt_cr(total * a.factor + a.eps);
+  uint16_t* yr = a.y + row * a.ldy;
+  for (int64_t j = tid; j < n; j += blockDim.x)
+    yr[j] = (uint16_t)f2bf(bf2f(a.w[j]) * rbf(src_val<ADD>(a, row, j) * rstd));
+}
+
+// LayerNorm with torch's vectorized kernel order for any n % 4 == 0: 256
+// threads per row, thread t pushes the 4-element vectors t, t + 256, ...; the
+// wavefront tree by shuffle-down (a lane past the end reads itself, as in
+// torch), the four wavefront results combined by thread 0.
+template <bool ADD>
+__global__ __launch_bounds__(256) void ln_torch_block_kernel(NormArgs a) {
+  __shared__ float wres[4][3];
+  __shared__ float stat[2];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & (kWave - 1);
+  write_sum<ADD>(a, row);
+  Wf s{0.0f, 0.0f, 0.0f};
+  for (int64_t v = t; v < a.n / 4; v += 256) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s = wf_push(s, src_val<ADD>(a, row, v * 4 + e));
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const Wf o{__shfl_down(s.mean, off, kWave), __shfl_down(s.m2, off, kWave),
+               __shfl_down(s.n, off, kWave)};
+    s = wf_combine<true>(s, o);
+  }
+  if (lane == 0) {
+    wres[t / kWave][0] = s.mean;
+    wres[t / kWave][1] = s.m2;
+    wres[t / kWave][2] = s.n;
+  }
+  __syncthreads();
+  if (t == 0) {
+    Wf w4[4];
+    for (int i = 0; i < 4; ++i) w4[i] = Wf{wres[i][0], wres[i][1], wres[i][2]};
+    w4[0] = wf_combine<false>(w4[0], w4[2]);
+    w4[1] = wf_combine<false>(w4[1], w4[3]);
+    w4[0] = wf_combine<false>(w4[0], w4[1]);
+    stat[0] = w4[0].mean;
+    stat[1] = __builtin_amdgcn_rsqf(w4[0].m2 / (float)a.n + a.eps);
+  }
+  __syncthreads();
+  const float mean = stat[0], rstd = stat[1];
+  uint16_t* yr = a.y + row * a.ldy;
+  for (int64_t j = t; j < a.n; j += blockDim.x) {
+    const float f = src_val<ADD>(a, row, j);
+    yr[j] = (uint16_t)f2bf(__builtin_fmaf(bf2f(a.w[j]), rstd * (f - mean), bf2f(a.b[j])));
+  }
+}
+
+// LayerNorm rows torch sends down its other kernel (n % 4 != 0, or a
+// contiguous input off 8-byte alignment): its order is not reproduced, so
+// these take exact statistics -- double sums of x and x^2 of bf16 data, exact
+// whatever the order, each rounded once to fp32; rsqrt correctly rounded.
 __device__ double block_sum(double v, double* red) {
   v = group_sum<kWave>(v);
   const int wid = threadIdx.x / kWave;
@@ -191,48 +565,25 @@ __device__ double block_sum(double v, double* red) {
   return t;
 }
 
-// Element j of the row the statistics are taken over: x, or bf16(x + r).
-// Recomputed on every pass (cheap, identical result) rather than re-read
-// from the summed output.
-template <int OP>
-__device__ __forceinline__ float src_val(const NormArgs& a, int64_t row, int64_t j) {
-  const float xf = bf2f(a.x[row * a.ldx + j]);
-  if constexpr (has_add(OP)) return rbf(xf + bf2f(a.r[row * a.ldr + j]));
-  return xf;
-}
-
-template <int OP>
-__global__ __launch_bounds__(256) void norm_generic_kernel(NormArgs a) {
+template <bool ADD>
+__global__ __launch_bounds__(256) void ln_exact_block_kernel(NormArgs a) {
   __shared__ double red[256 / kWave];
   const int64_t row = blockIdx.x;
-  if constexpr (has_add(OP)) {
-    uint16_t* sr = a.s + row * a.lds;
-    for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x)
-      sr[j] = (uint16_t)f2bf(src_val<OP>(a, row, j));
-  }
+  write_sum<ADD>(a, row);
   const double inv_n = 1.0 / (double)a.n;
-  float rstd, mean = 0.f;
   double sum = 0.0, ssq = 0.0;
   for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x) {
-    const float f = src_val<OP>(a, row, j);
-    if constexpr (is_ln(OP)) sum += (double)f;
+    const float f = src_val<ADD>(a, row, j);
+    sum += (double)f;
     ssq += (double)(f * f);
   }
-  if constexpr (is_ln(OP)) {
-    const double mean_d = block_sum(sum, red) * inv_n;
-    mean = (float)mean_d;
-    rstd = rsqrt_cr((float)(block_sum(ssq, red) * inv_n - mean_d * mean_d) + a.eps);
-  } else {
-    rstd = rsqrt_cr((float)(block_sum(ssq, red) * inv_n) + a.eps);
-  }
+  const double mean_d = block_sum(sum, red) * inv_n;
+  const float mean = (float)mean_d;
+  const float rstd = rsqrt_cr((float)(block_sum(ssq, red) * inv_n - mean_d * mean_d) + a.eps);
   uint16_t* yr = a.y + row * a.ldy;
   for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x) {
-    const float f = src_val<OP>(a, row, j);
-    const float w = bf2f(a.w[j]);
-    float o;
-    if constexpr (is_ln(OP)) o = __builtin_fmaf(w, rstd * (f - mean), bf2f(a.b[j]));
-    else o = w * rbf(f * rstd);
-    yr[j] = (uint16_t)f2bf(o);
+    const float f = src_val<ADD>(a, row, j);
+    yr[j] = (uint16_t)f2bf(__builtin_fmaf(bf2f(a.w[j]), rstd * (f - mean), bf2f(a.b[j])));
   }
 }
 
@@ -241,15 +592,20 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(NormArgs a) {
 // Block size: the hardware spreads workgroups evenly over the 256 CUs only
 // when there are many of them, so small row counts get 64- or 128-thread
 // blocks (the largest block that still yields >= 8 blocks per CU).
-template <int OP, int LPR, int MAXV, int RPG = 1>
-int launch_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
+inline int block_threads(int64_t lanes_total) {
   int threads = 256;
-  while (threads > 64 && (a.rows * LPR / RPG + threads - 1) / threads < 8 * 256) threads >>= 1;
+  while (threads > 64 && (lanes_total + threads - 1) / threads < 8 * 256) threads >>= 1;
+  return threads;
+}
+
+template <bool ADD, int LPR, int MAXV, int RPG = 1>
+int launch_rms_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
+  const int threads = block_threads(a.rows * LPR / RPG);
   const int rows_per_block = threads / LPR * RPG;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((norm_rows_kernel<OP, LPR, MAXV, RPG>), dim3((unsigned)blocks), dim3(threads),
-                     0, st, a, nvec, vpl);
+  hipLaunchKernelGGL((rms_rows_kernel<ADD, LPR, MAXV, RPG>), dim3((unsigned)blocks),
+                     dim3(threads), 0, st, a, nvec, vpl);
   return launch_status();
 }
 
@@ -259,62 +615,117 @@ int launch_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
 // smaller launches keep one row per group, spread over more wavefronts.
 constexpr int64_t kRpgMinThreads = (int64_t)256 * 16 * 64;
 
-template <int OP, int LPR, int MAXV>
-int launch_small_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
+template <bool ADD, int LPR, int MAXV>
+int launch_rms_small(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
   constexpr int kRpg = MAXV == 1 ? 4 : 2;
   if (a.rows * LPR / kRpg >= kRpgMinThreads)
-    return launch_rows<OP, LPR, MAXV, kRpg>(a, nvec, vpl, st);
-  return launch_rows<OP, LPR, MAXV>(a, nvec, vpl, st);
+    return launch_rms_rows<ADD, LPR, MAXV, kRpg>(a, nvec, vpl, st);
+  return launch_rms_rows<ADD, LPR, MAXV>(a, nvec, vpl, st);
 }
 
-template <int OP, int LPR>
-int launch_lpr(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
+constexpr int kRmsMaxVpl = 24;  // vectors per lane the register path holds
+
+template <bool ADD, int LPR>
+int launch_rms_lpr(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
   switch (vpl) {
-    case 1: return launch_small_rows<OP, LPR, 1>(a, nvec, vpl, st);
-    case 2: return launch_small_rows<OP, LPR, 2>(a, nvec, vpl, st);
-    case 3: return launch_rows<OP, LPR, 3>(a, nvec, vpl, st);
-    case 4: return launch_rows<OP, LPR, 4>(a, nvec, vpl, st);
-    case 5: return launch_rows<OP, LPR, 5>(a, nvec, vpl, st);
-    case 6: return launch_rows<OP, LPR, 6>(a, nvec, vpl, st);
+    case 1: return launch_rms_small<ADD, LPR, 1>(a, nvec, vpl, st);
+    case 2: return launch_rms_small<ADD, LPR, 2>(a, nvec, vpl, st);
+    case 3: return launch_rms_rows<ADD, LPR, 3>(a, nvec, vpl, st);
+    case 4: return launch_rms_rows<ADD, LPR, 4>(a, nvec, vpl, st);
+    case 5: return launch_rms_rows<ADD, LPR, 5>(a, nvec, vpl, st);
+    case 6: return launch_rms_rows<ADD, LPR, 6>(a, nvec, vpl, st);
     case 7:
-    case 8: return launch_rows<OP, LPR, 8>(a, nvec, vpl, st);
+    case 8: return launch_rms_rows<ADD, LPR, 8>(a, nvec, vpl, st);
     case 9:
-    case 10: return launch_rows<OP, LPR, 10>(a, nvec, vpl, st);
+    case 10: return launch_rms_rows<ADD, LPR, 10>(a, nvec, vpl, st);
     case 11:
-    case 12: return launch_rows<OP, LPR, 12>(a, nvec, vpl, st);
-    default: return launch_rows<OP, LPR, 16>(a, nvec, vpl, st);
+    case 12: return launch_rms_rows<ADD, LPR, 12>(a, nvec, vpl, st);
+    case 13:
+    case 14:
+    case 15:
+    case 16: return launch_rms_rows<ADD, LPR, 16>(a, nvec, vpl, st);
+    case 17:
+    case 18:
+    case 19:
+    case 20: return launch_rms_rows<ADD, LPR, 20>(a, nvec, vpl, st);
+    default: return launch_rms_rows<ADD, LPR, 24>(a, nvec, vpl, st);
   }
 }
 
-template <int OP>
-int launch_norm(const NormArgs& a, hipStream_t st) {
-  bool vec = a.n % 8 == 0 && a.ldx % 8 == 0 && a.ldy % 8 == 0 && aligned16(a.x) &&
-             aligned16(a.y) && aligned16(a.w);
-  if (has_add(OP)) vec = vec && a.ldr % 8 == 0 && a.lds % 8 == 0 && aligned16(a.r) && aligned16(a.s);
-  if (is_ln(OP)) vec = vec && aligned16(a.b);
+template <bool ADD>
+int launch_rms(NormArgs a, hipStream_t st) {
+  RmsPlan p;
+  if (!rms_plan(a.rows, a.n, p) || (p.split && p.bh > 16)) return UMIC_ERR_UNSUPPORTED;
+  a.factor = (float)a.rows / (float)(a.rows * a.n);
+  bool vec = p.vec && !p.split && p.bw <= kWave && a.n % 8 == 0 && a.ldx % 8 == 0 &&
+             a.ldy % 8 == 0 && aligned16(a.x) && aligned16(a.y) && aligned16(a.w);
+  if (ADD) vec = vec && a.ldr % 8 == 0 && a.lds % 8 == 0 && aligned16(a.r) && aligned16(a.s);
   const int64_t nvec = a.n / 8;
-  if (vec && nvec >= 8 && nvec <= 64 * 16) {
-    // Lanes per row: the widest group that splits the row evenly into at
-    // most 16 vectors per lane; else the widest group with a ragged tail.
-    int lpr = 0;
-    for (int g = 64; g >= 8 && !lpr; g >>= 1)
-      if (nvec % g == 0 && nvec / g <= 16) lpr = g;
-    if (!lpr) {
-      lpr = 8;
-      while (lpr * 2 <= 64 && lpr * 2 <= nvec) lpr *= 2;
-    }
-    const int vpl = (int)((nvec + lpr - 1) / lpr);
-    if (vpl <= 16) {
-      switch (lpr) {
-        case 64: return launch_lpr<OP, 64>(a, (int)nvec, vpl, st);
-        case 32: return launch_lpr<OP, 32>(a, (int)nvec, vpl, st);
-        case 16: return launch_lpr<OP, 16>(a, (int)nvec, vpl, st);
-        default: return launch_lpr<OP, 8>(a, (int)nvec, vpl, st);
-      }
-    }
+  const int lpr = p.bw / 2;
+  const int64_t vpl = vec ? (nvec + lpr - 1) / lpr : 0;
+  if (vec && vpl <= kRmsMaxVpl) {
+    if (lpr == 32) return launch_rms_lpr<ADD, 32>(a, (int)nvec, (int)vpl, st);
+    if (lpr == 16) return launch_rms_lpr<ADD, 16>(a, (int)nvec, (int)vpl, st);
   }
   if (a.rows > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((norm_generic_kernel<OP>), dim3((unsigned)a.rows), dim3(256), 0, st, a);
+  const int threads = p.bw * (p.split ? p.bh : 1);
+  hipLaunchKernelGGL((rms_block_kernel<ADD>), dim3((unsigned)a.rows), dim3(threads), 0, st, a,
+                     p);
+  return launch_status();
+}
+
+template <bool ADD, int M4>
+int launch_ln_rows(const NormArgs& a, int nvec4, hipStream_t st) {
+  const int threads = block_threads(a.rows * 16);
+  const int rows_per_block = threads / 16;
+  const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((ln_rows_kernel<ADD, M4>), dim3((unsigned)blocks), dim3(threads), 0, st, a,
+                     nvec4);
+  return launch_status();
+}
+
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+
+template <bool ADD>
+int launch_ln(const NormArgs& a, hipStream_t st) {
+  if (a.rows > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  // eager's layer_norm reads x itself when it is contiguous (else a fresh,
+  // aligned copy; the add form normalises a fresh sum), and takes its
+  // vectorized kernel for n % 4 == 0 with 8-byte aligned x, weight and bias
+  const bool contiguous = a.rows == 1 || a.ldx == a.n;
+  const bool torch_vec = a.n % 4 == 0 && a.n <= (1 << 24) && aligned8(a.w) && aligned8(a.b) &&
+                         (ADD || !contiguous || aligned8(a.x));
+  if (!torch_vec) {
+    hipLaunchKernelGGL((ln_exact_block_kernel<ADD>), dim3((unsigned)a.rows), dim3(256), 0, st,
+                       a);
+    return launch_status();
+  }
+  bool vec = a.ldx % 4 == 0 && a.ldy % 4 == 0 && aligned8(a.x) && aligned8(a.y);
+  if (ADD) vec = vec && a.ldr % 4 == 0 && a.lds % 4 == 0 && aligned8(a.r) && aligned8(a.s);
+  const int nvec4 = (int)(a.n / 4);
+  if (vec) {
+    switch ((nvec4 + 63) / 64) {  // register slots / 4
+      case 1: return launch_ln_rows<ADD, 1>(a, nvec4, st);
+      case 2: return launch_ln_rows<ADD, 2>(a, nvec4, st);
+      case 3: return launch_ln_rows<ADD, 3>(a, nvec4, st);
+      case 4: return launch_ln_rows<ADD, 4>(a, nvec4, st);
+      case 5: return launch_ln_rows<ADD, 5>(a, nvec4, st);
+      case 6: return launch_ln_rows<ADD, 6>(a, nvec4, st);
+      case 7:
+      case 8: return launch_ln_rows<ADD, 8>(a, nvec4, st);
+      case 9:
+      case 10: return launch_ln_rows<ADD, 10>(a, nvec4, st);
+      case 11:
+      case 12: return launch_ln_rows<ADD, 12>(a, nvec4, st);
+      case 13:
+      case 14:
+      case 15:
+      case 16: return launch_ln_rows<ADD, 16>(a, nvec4, st);
+      default: break;
+    }
+  }
+  hipLaunchKernelGGL((ln_torch_block_kernel<ADD>), dim3((unsigned)a.rows), dim3(256), 0, st, a);
   return launch_status();
 }
 
@@ -327,7 +738,8 @@ int norm_entry(NormArgs a, void* stream) {
   if (is_ln(OP) && !a.b) return UMIC_ERR_INVALID_ARG;
   if (a.ldx < a.n || a.ldy < a.n) return UMIC_ERR_INVALID_ARG;
   if (has_add(OP) && (a.ldr < a.n || a.lds < a.n)) return UMIC_ERR_INVALID_ARG;
-  return launch_norm<OP>(a, as_stream(stream));
+  if constexpr (is_ln(OP)) return launch_ln<has_add(OP)>(a, as_stream(stream));
+  return launch_rms<has_add(OP)>(a, as_stream(stream));
 }
 
 }  // namespace
@@ -338,7 +750,7 @@ using namespace umic;
 extern "C" int umic_rmsnorm_bf16(const void* x, const void* w, void* y, int64_t rows, int64_t n,
                                  int64_t ldx, int64_t ldy, float eps, void* stream) {
   NormArgs a{(const uint16_t*)x, nullptr, (const uint16_t*)w, nullptr, (uint16_t*)y, nullptr,
-             rows, n, ldx, 0, ldy, 0, eps};
+             rows, n, ldx, 0, ldy, 0, eps, 0.0f};
   return norm_entry<kRms>(a, stream);
 }
 
@@ -347,7 +759,7 @@ extern "C" int umic_add_rmsnorm_bf16(const void* x, const void* r, const void* w
                                      int64_t ldr, int64_t ldn, int64_t lds, float eps,
                                      void* stream) {
   NormArgs a{(const uint16_t*)x, (const uint16_t*)r, (const uint16_t*)w, nullptr,
-             (uint16_t*)normed, (uint16_t*)summed, rows, n, ldx, ldr, ldn, lds, eps};
+             (uint16_t*)normed, (uint16_t*)summed, rows, n, ldx, ldr, ldn, lds, eps, 0.0f};
   return norm_entry<kAddRms>(a, stream);
 }
 
@@ -355,7 +767,7 @@ extern "C" int umic_layernorm_bf16(const void* x, const void* w, const void* b, 
                                    int64_t rows, int64_t n, int64_t ldx, int64_t ldy, float eps,
                                    void* stream) {
   NormArgs a{(const uint16_t*)x, nullptr, (const uint16_t*)w, (const uint16_t*)b, (uint16_t*)y,
-             nullptr, rows, n, ldx, 0, ldy, 0, eps};
+             nullptr, rows, n, ldx, 0, ldy, 0, eps, 0.0f};
   return norm_entry<kLn>(a, stream);
 }
 
@@ -364,6 +776,6 @@ extern "C" int umic_add_layernorm_bf16(const void* x, const void* r, const void*
                                        int64_t n, int64_t ldx, int64_t ldr, int64_t ldn,
                                        int64_t lds, float eps, void* stream) {
   NormArgs a{(const uint16_t*)x, (const uint16_t*)r, (const uint16_t*)w, (const uint16_t*)b,
-             (uint16_t*)normed, (uint16_t*)summed, rows, n, ldx, ldr, ldn, lds, eps};
+             (uint16_t*)normed, (uint16_t*)summed, rows, n, ldx, ldr, ldn, lds, eps, 0.0f};
   return norm_entry<kAddLn>(a, stream);
 }

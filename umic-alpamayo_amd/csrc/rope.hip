@@ -50,7 +50,7 @@ struct RopeArgs {
   const uint16_t* qw;
   const uint16_t* kw;
   float eps;
-  double inv_d;          // 1 / D
+  float fq, fk;          // MeanOps factors of the q and k head rows (see rms_norm_chunks)
 };
 
 // Items per position are bounded (checked on the host) so that every
@@ -239,34 +239,38 @@ template <bool NORM>
 constexpr int direct_items() { return NORM ? 1 : 2; }
 constexpr int kKvItems = 1;
 
-// RMSNorm of a head row ahead of its rotation: the text attention's q_norm /
-// k_norm, HF Qwen3VLTextRMSNorm, bf16(w * bf16(x * rsqrt(mean(x^2) + eps))).
-// A head row is G = D/16 items, one per lane, on G consecutive lanes that
-// start at a multiple of G (rows start at multiples of G items and a block's
-// items are lane-ordered); each lane holds chunk c of both halves.  The sum
-// of squares is exact in double for bf16 data, so the butterfly order does
-// not change it: every lane of the row gets the row's statistics as a serial
-// sum would, the mean is rounded once to fp32 and the reciprocal square root
-// is correctly rounded -- the norm kernel's numerics.  Called with the whole
-// row active (rows are skipped or kept as a unit).
+// HF Qwen3VLTextRMSNorm of one head row ahead of its rotation (the text
+// attention's q_norm / k_norm), in place.  A head row is G = D/16 items, one
+// per lane, on G consecutive lanes that start at a multiple of G (rows start
+// at multiples of G items and a block's items are lane-ordered): lane c holds
+// the chunks [8c, 8c + 8) (xl) and [D/2 + 8c, +8) (xh); w holds the matching
+// weight chunks.  Called with the whole row active (rows are skipped or kept
+// as a unit).  The statistic follows torch-ROCm's reduction for
+// rows of D = 128 or 256 (aten Reduce.cuh, 4-element vectors, D/4 reducing
+// threads of one vector each): thread t sums the squares of elements 4t..4t+3
+// in order; the threads combine in adjacent pairs, pairs of pairs, ... --
+// here threads 2c, 2c + 1 in-lane, then a butterfly over the G lanes for
+// each half row, and last the two halves.  mean = sum * factor (MeanOps:
+// float(rows) / float(rows * D)), rstd correctly rounded, then
+// bf16(w * bf16(x * rstd)).  G is launch-uniform.
+__device__ __forceinline__ float quad_sq(const float* v) {
+  return ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
+}
+
+__device__ __forceinline__ float row_sum_dpp(float v, int G) {
+  v += dpp_move<0xB1>(v);                // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_move<0x4E>(v);                // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp_move<0x141>(v);               // row_half_mirror: the other quad of 8
+  if (G >= 16) v += dpp_move<0x140>(v);  // row_mirror: the other 8 of 16
+  return v;
+}
+
 __device__ __forceinline__ void rms_norm_chunks(float (&xl)[8], float (&xh)[8],
-                                                const u32x4 (&w)[2], int G, double inv_d,
+                                                const u32x4 (&w)[2], int G, float factor,
                                                 float eps) {
-  // four partial sums: shorter dependency chains, same exact total
-  double s4[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) s4[e & 3] += (double)(xl[e] * xl[e]) + (double)(xh[e] * xh[e]);
-  double ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-  // butterfly within the row's G lanes: DPP moves inside a 16-lane row (full
-  // rate, no LDS crossbar), then shuffles for G = 32, 64.  After the quad
-  // steps every lane of a quad holds the quad sum, so the half-row and row
-  // mirrors add the partner quad / half.  G is launch-uniform.
-  if (G >= 2) ss += dpp_move<0xB1>(ss);   // quad_perm [1,0,3,2]: lane ^ 1
-  if (G >= 4) ss += dpp_move<0x4E>(ss);   // quad_perm [2,3,0,1]: lane ^ 2
-  if (G >= 8) ss += dpp_move<0x141>(ss);  // row_half_mirror: lane ^ 7 in 8
-  if (G >= 16) ss += dpp_move<0x140>(ss); // row_mirror: lane ^ 15 in 16
-  for (int m = 16; m < G; m <<= 1) ss += __shfl_xor(ss, m, kWave);
-  const float rstd = rsqrt_cr((float)(ss * inv_d) + eps);
+  const float lo = row_sum_dpp(quad_sq(xl) + quad_sq(xl + 4), G);
+  const float hi = row_sum_dpp(quad_sq(xh) + quad_sq(xh + 4), G);
+  const float rstd = rsqrt_cr((lo + hi) * factor + eps);
   float wl[8], wh[8];
   unpack8(w[0], wl);
   unpack8(w[1], wh);
@@ -369,7 +373,8 @@ __global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
     float xl[VEC], xh[VEC];
     unpack8(rl[u], xl);
     unpack8(rh[u], xh);
-    if constexpr (NORM) rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, a.inv_d, a.eps);
+    if constexpr (NORM)
+      rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, qrow[u] ? a.fq : a.fk, a.eps);
     float cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
     unpack8(tb[u].cs[0], cl);
     unpack8(tb[u].cs[1], ch);
@@ -407,7 +412,7 @@ struct KvArgs {
   const uint16_t* qw;    // RMSNorm of q / k head rows (norm kernel only)
   const uint16_t* kw;
   float eps;
-  double inv_d;          // 1 / D
+  float fq, fk;          // MeanOps factors of the q and k head rows
 };
 
 template <bool NORM = false>
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvArgs a) {
     unpack8(rl[u], xl);
     unpack8(rh[u], xh);
     if constexpr (NORM)
-      rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, a.inv_d, a.eps);
+      rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, kind[u] == 0 ? a.fq : a.fk, a.eps);
     unpack8(tb[u].cs[0], cl);
     unpack8(tb[u].cs[1], ch);
     unpack8(tb[u].cs[2], sl);
@@ -611,11 +616,15 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
 namespace umic {
 namespace {
 
-// head_dim values the fused RMSNorm takes: 16-byte chunks (D % 16 == 0) and
-// a row group of D/16 lanes that is a power of two within one wavefront.
-bool norm_dim_ok(int64_t D) {
-  const int64_t g = D / 16;
-  return D % 16 == 0 && g >= 1 && g <= kWave && (g & (g - 1)) == 0;
+// head_dim values the fused RMSNorm takes: D = 128 or 256, whose eager
+// reduction (one 4-element vector per reducing thread, whatever the row
+// count) rms_norm_chunks reproduces; other head sizes normalise with
+// umic_rmsnorm_bf16 first.
+bool norm_dim_ok(int64_t D) { return D == 128 || D == 256; }
+
+// aten MeanOps factor of `rows` head rows of D: float(rows) / float(rows * D)
+float mean_factor(int64_t rows, int64_t D) {
+  return rows > 0 ? (float)rows / (float)(rows * D) : 0.0f;
 }
 
 // The in-place cache append, optionally with the q / k RMSNorm (qw, kw
@@ -648,7 +657,8 @@ int kv_append_impl(const void* q, const void* k, const void* v, void* q_out, voi
            pos_dev, B, S, Hq, Hk, D, q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh,
            qo_sb, qo_ss, qo_sh, c_sb, c_sh, c_ss, capacity, pos, cs_sb, cs_ss,
            small_div((int)((Hq + 2 * Hk) * (D / 16))), small_div((int)(D / 16)),
-           (const uint16_t*)qw, (const uint16_t*)kw, eps, 1.0 / (double)D};
+           (const uint16_t*)qw, (const uint16_t*)kw, eps, mean_factor(B * S * Hq, D),
+           mean_factor(B * S * Hk, D)};
   bool ok = cs_sb % 8 == 0 && cs_ss % 8 == 0 && (uintptr_t)cos % 16 == 0 &&
             (uintptr_t)sin % 16 == 0;
   if (Hq) {
@@ -747,7 +757,8 @@ extern "C" int umic_qk_rmsnorm_rope_bf16(const void* q, const void* k, void* q_o
   a.qw = (const uint16_t*)q_w;
   a.kw = (const uint16_t*)k_w;
   a.eps = eps;
-  a.inv_d = 1.0 / (double)D;
+  a.fq = mean_factor(B * S * Hq, D);
+  a.fk = mean_factor(B * S * Hk, D);
   const int64_t nitems = B * S * (Hq + Hk) * (D / 16);
   constexpr int per_block = direct_items<true>() * 256;
   const int64_t blocks = (nitems + per_block - 1) / per_block;

@@ -256,11 +256,11 @@ def kv_launch(q, k, v, cos, sin, k_cache, v_cache, pos: int,
 
 def norm_weights_ok(q, q_w, k_w) -> bool:
     """Head-row RMSNorm weights the fused norm + RoPE kernels take: [D] bf16,
-    contiguous, 16-byte aligned, on q's device, with D/16 a power of two up to
-    64 (one row per aligned group of D/16 lanes)."""
+    contiguous, 16-byte aligned, on q's device, with D = 128 or 256 -- the head
+    sizes whose eager q_norm / k_norm reduction order the kernels reproduce
+    (other sizes run the module norms, then the fused RoPE)."""
     D = q.shape[-1]
-    g = D // 16
-    if D % 16 or not 1 <= g <= 64 or g & (g - 1):
+    if D not in (128, 256):
         return False
     return all(isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16 and w.dim() == 1
                and w.shape[0] == D and w.is_contiguous() and w.device == q.device
