@@ -3,8 +3,8 @@
 The in-place cache must be observably the same cache as the concatenating
 DynamicCache the reference replaces (src/umic/cache.py): the same keys and
 values after every append and crop, the same model outputs when a text model
-runs on it, an overflow error instead of a silent grow, and the graph-mode
-write at a device-held position.  On the CPU the fused-attention patch
+runs on it, an overflow error instead of a silent grow, and the replay-time
+write at a device-held cursor.  Its storage is one arena per layer geometry.  On the CPU the fused-attention patch
 (``fuse_kv_rope``) takes its eager branch, so these tests also pin that branch
 (RoPE through transformers, then ``update``) against the unpatched model.
 """
@@ -16,7 +16,7 @@ import torch
 from transformers.cache_utils import DynamicCache, DynamicLayer
 
 from umic import integrate
-from umic.cache import InplaceKVCache, InplaceLayer
+from umic.cache import InplaceKVCache, InplaceLayer, KVArena
 
 pytestmark = pytest.mark.filterwarnings("ignore::FutureWarning")
 BF = torch.bfloat16
@@ -46,9 +46,10 @@ def test_inplace_layer_tracks_dynamic_layer_through_appends_and_crops():
     ref = DynamicLayer()
     k0, v0 = kv(B, H, 6, D, 0)
     ref.update(k0, v0)
-    kb, vb = torch.zeros(B, H, cap, D, dtype=BF), torch.zeros(B, H, cap, D, dtype=BF)
-    kb[:, :, :6], vb[:, :, :6] = k0, v0
-    lyr = InplaceLayer(kb, vb, 6)
+    arena = KVArena(1, B, H, cap, D, BF, "cpu")
+    lyr = InplaceLayer(arena, 0)
+    lyr.update(k0, v0)
+    kb = arena.k(0)
     steps = [("add", 5), ("add", 1), ("crop", 8), ("add", 3), ("crop", -2), ("add", 1),
              ("add", 7), ("crop", 0), ("add", 2)]
     for i, (op, n) in enumerate(steps):
@@ -71,18 +72,36 @@ def test_inplace_layer_tracks_dynamic_layer_through_appends_and_crops():
             lyr.crop(n)
         assert lyr.get_seq_length() == ref.get_seq_length()
         assert torch.equal(lyr.keys, ref.keys) and torch.equal(lyr.values, ref.values)
-    assert lyr.get_max_length() == cap and kb.data_ptr() == lyr._k_buf.data_ptr()
+    assert lyr.get_max_length() == cap and kb.data_ptr() == arena.storage.data_ptr()
 
 
 def test_overflow_raises_and_keeps_the_cache():
-    kb, vb = torch.zeros(1, 2, 8, 4, dtype=BF), torch.zeros(1, 2, 8, 4, dtype=BF)
-    lyr = InplaceLayer(kb, vb, 6)
+    arena = KVArena(1, 1, 2, 8, 4, BF, "cpu")
+    arena.storage.zero_()
+    lyr = InplaceLayer(arena, 0)
+    lyr.update(*kv(1, 2, 6, 4, 0))
     k, v = kv(1, 2, 3, 4, 1)
     with pytest.raises(RuntimeError, match="overflow"):
         lyr.update(k, v)
-    assert lyr.get_seq_length() == 6 and not kb[:, :, 6:].any()
+    assert lyr.get_seq_length() == 6 and not arena.k(0)[:, :, 6:].any()
     with pytest.raises(ValueError):
-        InplaceLayer(kb, vb, 9)
+        KVArena(1, 1, 0, 8, 4, BF, "cpu")
+
+
+def test_arena_layout_one_allocation():
+    """Every layer of one geometry lives in one allocation: k and v of a layer
+    are adjacent views with equal strides (what the fused append writes)."""
+    dyn = DynamicCache()
+    for i in range(4):
+        dyn.update(*kv(1, 2, 5, 8, i), layer_idx=i)
+    conv = InplaceKVCache.from_dynamic(dyn, extra_tokens=3, margin=0)
+    assert len(conv.arenas) == 1
+    ar = conv.arenas[0]
+    assert tuple(ar.storage.shape) == (4, 2, 1, 2, 8, 8)
+    for i, lyr in enumerate(conv.layers):
+        assert lyr.arena is ar and lyr.index == i
+        assert ar.k(i).stride() == ar.v(i).stride()
+        assert ar.v(i).data_ptr() - ar.k(i).data_ptr() == ar.k(i).numel() * 2
 
 
 def test_from_dynamic_copies_the_prefix_once():
@@ -96,7 +115,7 @@ def test_from_dynamic_copies_the_prefix_once():
         assert lyr.capacity == S + 10 + 4
         assert torch.equal(lyr.keys, dyn.layers[i].keys)
         assert torch.equal(lyr.values, dyn.layers[i].values)
-        assert lyr._k_buf.data_ptr() != dyn.layers[i].keys.data_ptr()
+        assert lyr.arena.k(lyr.index).data_ptr() != dyn.layers[i].keys.data_ptr()
     conv.update(*kv(B, H, 3, D, 9), layer_idx=1)
     assert conv.get_seq_length(1) == S + 3 and conv.get_seq_length(0) == S
     conv.crop(S)
@@ -104,23 +123,45 @@ def test_from_dynamic_copies_the_prefix_once():
     assert conv.get_seq_length(7) == 0
 
 
-def test_graph_mode_writes_at_the_device_position():
-    B, H, D, cap = 1, 2, 8, 12
+def test_replay_writes_at_the_device_cursor():
+    B, H, D = 1, 2, 8
     dyn = DynamicCache()
     dyn.update(*kv(B, H, 4, D, 0), layer_idx=0)
     conv = InplaceKVCache.from_dynamic(dyn, extra_tokens=4, margin=0)
-    pos_t = torch.tensor([6])
-    conv.enable_graph_mode(pos_t)
-    conv.set_graph_len(7)
+    assert conv.layers[0].capacity == 8
+    cursor = torch.tensor([6])
+    conv.replay_at(cursor, 7)
     k, v = kv(B, H, 1, D, 3)
     rk, rv = conv.update(k, v, 0)
     assert rk.shape[2] == 7 and rk.is_contiguous()
     assert torch.equal(rk[:, :, 6:7], k) and torch.equal(rv[:, :, 6:7], v)
-    assert conv.get_seq_length() == 4          # the host pointer is synced separately
-    conv.set_pos(7)
-    conv.disable_graph_mode()
-    assert conv.layers[0].keys.shape[2] == 7 and cap == 4 + 4 + 4
+    assert conv.get_seq_length() == 4          # the host fill is set separately
+    conv.set_length(7)
+    conv.end_replay()
+    assert conv.layers[0].keys.shape[2] == 7
     assert torch.equal(conv.layers[0].keys[:, :, 6:7], k)
+    # a multi-token write during replay goes to the host fill, as eagerly
+    conv.replay_at(cursor, 7)
+    conv.update(*kv(B, H, 1, D, 4), 0)
+    conv.end_replay()
+    conv.update(*kv(B, H, 1, D, 5), 0)
+    assert conv.get_seq_length() == 8
+
+
+def test_reseed_keeps_the_buffers():
+    """A new inference with the same prompt length is copied into the same
+    arena, so addresses baked into captured graphs stay valid."""
+    d1, d2 = DynamicCache(), DynamicCache()
+    for i in range(2):
+        d1.update(*kv(1, 2, 5, 8, i), layer_idx=i)
+        d2.update(*kv(1, 2, 5, 8, 10 + i), layer_idx=i)
+    conv = InplaceKVCache.from_dynamic(d1, extra_tokens=4)
+    ptr = conv.arenas[0].storage.data_ptr()
+    conv.update(*kv(1, 2, 2, 8, 7), layer_idx=0)
+    conv.reseed(d2)
+    assert conv.arenas[0].storage.data_ptr() == ptr and conv.get_seq_length() == 5
+    for a, b in zip(conv.layers, d2.layers):
+        assert torch.equal(a.keys, b.keys) and torch.equal(a.values, b.values)
 
 
 def test_text_model_on_the_inplace_cache_matches_dynamic_cache():
@@ -206,7 +247,7 @@ def test_decode_graph_runner_passes_cpu_calls_through():
         runner = DecodeGraphRunner(m, max_new_tokens=8)
         out = m.generate(**kw)
     assert torch.equal(out, ref)
-    assert runner.replays == 0 and not runner.graphs and runner.cache is None
+    assert runner.replays == 0 and not len(runner.graphs) and runner.cache is None
 
 
 def test_flow_step_graph_falls_back_to_eager_on_cpu():
@@ -226,7 +267,7 @@ def test_flow_step_graph_falls_back_to_eager_on_cpu():
     for i, x in enumerate(xs):
         t = torch.full((1,), float(i))
         assert torch.equal(fsg(x, t), x * 2 + t)
-    assert fsg.failed and fsg.graph is None and len(calls) == 5
+    assert fsg.disabled and not fsg.captured and len(calls) == 5
 
     class Diffusion:
         def sample(self, noise, step_fn=None, unguided_step_fn=None):

@@ -5,8 +5,10 @@ greedy generate():
 
 The same prompts are decoded eagerly by the unpatched model first; then the
 LM gets the fused kernels (RMSNorm, add+RMSNorm, text RoPE, RoPE + in-place
-KV append) and the runner, and every generation must produce the eager
-tokens, with per-step scores equal within bf16 noise.  Four inferences: the
+KV append, the q/k/v projections as one GEMV launch, q/o GEMVs, the P5 MLP
+GEMV with the residual add in down_proj's epilogue) and the runner, and every
+generation must produce the eager tokens, with per-step scores equal within
+bf16 noise.  Four inferences: the
 first warms up for two steps and captures one graph per remaining KV length,
 the second (same prompt length, new prompt, on the persistent buffers)
 captures the two warm-up lengths, the third is pure replay, the fourth (new
@@ -39,10 +41,10 @@ def small_vlm():
 
     cfg = Qwen3VLConfig(
         text_config=dict(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
-                         num_attention_heads=4, num_key_value_heads=4, head_dim=64,
+                         num_attention_heads=4, num_key_value_heads=4, head_dim=128,
                          vocab_size=512, rope_parameters={"rope_type": "default",
                                                           "rope_theta": 1e6,
-                                                          "mrope_section": [16, 8, 8],
+                                                          "mrope_section": [24, 20, 20],
                                                           "mrope_interleaved": True}),
         vision_config=dict(depth=1, hidden_size=64, num_heads=4, intermediate_size=128,
                            out_hidden_size=256, patch_size=4, temporal_patch_size=2,
@@ -77,6 +79,7 @@ def test_decode_graph_runner_matches_eager(monkeypatch):
         lm = m.model.language_model
         assert integrate.fuse_rmsnorms(lm) > 0 and integrate.fuse_add_rmsnorm(lm) == 2
         assert integrate.fuse_text_rope() and integrate.fuse_kv_rope(lm) == 2
+        assert integrate.fuse_mlps(lm) == 2 and integrate.fuse_linears(lm) == 4
         runner = DecodeGraphRunner(m, max_new_tokens=NEW)
         log = collections.Counter()
         real = _lib.call
@@ -98,6 +101,7 @@ def test_decode_graph_runner_matches_eager(monkeypatch):
                 assert err <= 2e-2, (i, float(err))
         finally:
             integrate.unfuse_rope()
+            integrate.unfuse_mlps(lm)
     # NEW - 1 decode steps per inference (the first token comes from prefill);
     # with no graphs yet, the first two steps are eager warm-up
     assert captured == [NEW - 3, NEW - 1, NEW - 1, NEW - 3]
@@ -106,6 +110,9 @@ def test_decode_graph_runner_matches_eager(monkeypatch):
     # fused at prefill
     assert log["umic_qk_rmsnorm_rope_kv_append_bf16"] > 0
     assert log["umic_qk_rmsnorm_rope_bf16"] > 0
+    # the decode GEMVs: q/k/v in one launch, the P5 MLP, down_proj + residual
+    for name in ("umic_linear_multi_bf16", "umic_gate_silu_mul_bf16", "umic_linear_add_bf16"):
+        assert log[name] > 0, name
 
 
 def test_flow_step_graph_replays_match_eager():
@@ -149,6 +156,6 @@ def test_flow_step_graph_replays_match_eager():
             out = fsg(x, t)
             torch.cuda.synchronize()
             assert torch.equal(out, ref), i
-        assert fsg.graph is not None and not fsg.failed
-        assert torch.equal(cache.layers[0]._k_buf[:, :, :P], prefix_k)
+        assert fsg.captured and not fsg.disabled
+        assert torch.equal(cache.arenas[0].k(0)[:, :, :P], prefix_k)
     integrate.unfuse_mlps(layer)

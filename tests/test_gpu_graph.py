@@ -37,6 +37,8 @@ def _inputs(seed):
         "vr": bf16_randn(64, 1280, gen=g),
         "x": bf16_randn(128, 512, gen=g),
         "xs": bf16_randn(300, 12288, gen=g),
+        "hd": bf16_randn(1, 2, 512, gen=g),    # decode rows for the GEMVs
+        "hr": bf16_randn(1, 2, 512, gen=g),
     }
 
 
@@ -54,6 +56,12 @@ def _step(t, p):
     out["lin"] = linear.linear_hip(t["x"], p["wl"])
     out["lin_sk"] = linear.linear_hip(t["xs"], p["wsk"])  # stream-K schedule
     out["p5"] = fused_ffn.gate_silu_mul_hip(t["x"], p["wg"].t(), p["wu"].t())
+    # decode GEMVs: one linear, three in one launch, P5, down_proj + residual
+    out["gv"] = linear.linear_hip(t["hd"], p["wl"])
+    out["mq"], out["mk"], out["mv"] = linear.linear_multi_hip(
+        t["hd"], [p["wl"], p["wg"], p["wu"]], [None, p["bg"], None])
+    out["gp5"] = fused_ffn.gate_silu_mul_hip(t["hd"], p["wg"].t(), p["wu"].t())
+    out["gadd"] = linear.linear_add_hip(out["gp5"], p["wd"], None, t["hr"])
     return out
 
 
@@ -68,6 +76,8 @@ def test_fused_kernels_replay_in_hip_graph():
         "wg": bf16_randn(384, 512, scale=0.05, gen=g).to(DEV),
         "wu": bf16_randn(384, 512, scale=0.05, gen=g).to(DEV),
         "wsk": bf16_randn(264, 12288, scale=0.02, gen=g).to(DEV),
+        "bg": bf16_randn(384, scale=0.1, gen=g).to(DEV),
+        "wd": bf16_randn(512, 384, scale=0.05, gen=g).to(DEV),
     }
     from umic import _lib
 

@@ -166,9 +166,9 @@ def test_device_position_replays_in_a_captured_graph():
     assert np.array_equal(bits(vc)[:, :, rest], bits(vc0)[:, :, rest])
 
 
-def test_inplace_layer_graph_mode_append_matches_update():
-    """InplaceLayer.append_rotary in graph mode = transformers RoPE +
-    InplaceLayer.update (index_copy_ at the device position)."""
+def test_inplace_layer_replay_append_matches_update():
+    """InplaceLayer.append_rotary during replay = transformers RoPE +
+    InplaceLayer.update (index_copy_ at the device cursor)."""
     from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
 
     from transformers.cache_utils import DynamicCache
@@ -183,9 +183,8 @@ def test_inplace_layer_graph_mode_append_matches_update():
         dyn.update(prefix_k, prefix_v, 0)
         c = InplaceKVCache.from_dynamic(dyn, extra_tokens=8)
         # the token goes right after the prefix, so rows [0, base] are all
-        # defined and the graph length covers exactly them
-        c.enable_graph_mode(torch.tensor([base], dtype=torch.int64, device=DEV))
-        c.set_graph_len(base + 1)
+        # defined and the replay window covers exactly them
+        c.replay_at(torch.tensor([base], dtype=torch.int64, device=DEV), base + 1)
         caches.append(c)
     q = bf16_randn(B, 1, Hq, D, gen=g).to(DEV).transpose(1, 2)
     k = bf16_randn(B, 1, Hk, D, gen=g).to(DEV).transpose(1, 2)

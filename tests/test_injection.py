@@ -405,7 +405,7 @@ def test_apply_twice_is_idempotent():
     second = optimize.apply(model)
     assert second == first
     assert model.vlm.forward._umic_runner is runner
-    assert runner.orig_forward.__self__ is model.vlm
+    assert runner.wrapped_forward.__self__ is model.vlm
     assert len(model.expert._forward_pre_hooks) == hooks == 1
     integrate.unfuse_rope()
 
@@ -420,3 +420,33 @@ def test_find_lm_module_variants():
     root.vlm.language_model = outer
     assert optimize.find_lm_module(root) is outer
     assert optimize.find_lm_module(nn.Linear(2, 2)) is None
+
+
+def test_decode_paths_defer_to_hooked_modules():
+    """The decode paths call kernels in place of submodule calls only while
+    no forward hook would be skipped: a module hook, a pre-hook or a global
+    hook sends them back through the module's own __call__."""
+    lm = tiny_text_model()
+    attn, mlp = lm.layers[0].self_attn, lm.layers[0].mlp
+    assert not integrate._hooked(attn.q_proj, mlp, mlp.down_proj)
+    seen = []
+    h = attn.k_proj.register_forward_hook(lambda m, a, o: seen.append(m))
+    assert integrate._hooked(attn.q_proj, attn.k_proj) and not integrate._hooked(attn.q_proj)
+    h.remove()
+    h = mlp.register_forward_pre_hook(lambda m, a: None)
+    assert integrate._hooked(mlp, mlp.down_proj)
+    h.remove()
+    g = nn.modules.module.register_module_forward_hook(lambda m, a, o: None)
+    try:
+        assert integrate._hooked(attn.q_proj)
+    finally:
+        g.remove()
+    assert not integrate._hooked(attn.q_proj, attn.k_proj, mlp, mlp.down_proj)
+    # a hooked projection still fires on the fused attention path
+    assert integrate.fuse_kv_rope(lm) == 2
+    h = attn.k_proj.register_forward_hook(lambda m, a, o: seen.append(m))
+    with torch.no_grad():
+        lm(input_ids=torch.arange(6)[None])
+    h.remove()
+    integrate.unfuse_mlps(lm)
+    assert seen == [attn.k_proj]

@@ -1,212 +1,251 @@
-"""In-place KV cache with the text RoPE fused into the append.
+"""In-place KV cache for repeated decode / flow steps, written by the fused
+RoPE + append kernel.
 
-Same API and semantics as the reference's cache (src/umic/cache.py): an
-``InplaceLayer`` holds one layer's keys and values in a buffer allocated once
-([B, Hkv, capacity, D], from ``InplaceKVCache.from_dynamic``), ``update``
-writes new tokens in place instead of concatenating, and ``crop`` only moves
-the write pointer.  Returned keys/values are prefix views of the buffer --
-contiguous copies for single-token steps and in graph mode, where the write
-goes to a device-held position (replay-safe) and the exact graph length is
-returned.
+Storage.  A ``KVArena`` is one device allocation holding every layer's keys
+and values, ``[layers, 2, batch, kv_heads, capacity, head_dim]``: each
+layer's k and v are adjacent views with identical strides (what the fused
+append kernel writes), and converting or re-seeding a cache is one copy per
+layer into memory that never moves.  The arena keeps each layer's fill level
+on the host, and -- for graph replay -- one device int64 write cursor and
+one attention window shared by all layers: a replayed single-token step
+writes its row at the cursor and hands attention exactly ``window`` rows.
 
-What this build adds is ``InplaceLayer.append_rotary``: the attention's
-``apply_rotary_pos_emb`` and ``update`` in ONE gfx950 launch
-(``umic_rope_kv_append_bf16``) that rotates q, rotates k straight into the
-cache buffer and copies v beside it -- no rotated-k temporary, no separate
-copy kernels.  ``umic.integrate.fuse_kv_rope`` routes the text attention
-modules through it whenever their cache is an ``InplaceKVCache``.
+Writes.  ``InplaceLayer.append_rotary(q, k, v, cos, sin, norm)`` is the
+primary path: one launch rotates q, rotates k straight into the layer's key
+rows, copies v beside it, and (with ``norm``) applies the attention's q_norm /
+k_norm first (``umic_qk_rmsnorm_rope_kv_append_bf16``); under replay it
+writes at the arena cursor.  ``update(k, v)`` takes already-rotated keys --
+the interface transformers' attention calls -- and writes the same rows.
+
+Observable behaviour is the reference's in-place cache
+(src/umic/cache.py:25-160), which this replaces: keys/values are the
+prefix of the buffer (strided views; single-token steps and replays return
+contiguous copies), ``crop`` is O(1), a write past the capacity raises
+instead of growing, and ``InplaceKVCache`` is a transformers DynamicCache,
+so mask and attention back-end selection are unchanged.
 """
 
 from __future__ import annotations
-
-import logging
 
 import torch
 from transformers.cache_utils import DynamicCache, DynamicLayer
 
 from umic.kernels import rope
 
-logger = logging.getLogger(__name__)
 
+class KVArena:
+    """Keys and values of ``layers`` layers in one allocation.
 
-class InplaceLayer(DynamicLayer):
-    """One layer's KV in a pre-allocated buffer; appends are copy-free.
-
-    Follows src/umic/cache.py:25-91.  ``keys``/``values`` are strided prefix
-    views of the buffers (no ``.contiguous()`` on the multi-token path: that
-    would re-copy the prefix).
+    ``fill[i]`` tokens of layer i are valid (rows 0 .. fill[i] - 1).  While
+    ``cursor`` is set (a device int64 [1] tensor) single-token writes go to
+    row ``cursor`` and attention sees ``window`` rows.
     """
 
-    def __init__(self, k_buf: torch.Tensor, v_buf: torch.Tensor, base_len: int) -> None:
-        super().__init__()
-        if k_buf.shape != v_buf.shape or k_buf.dim() != 4:
-            raise ValueError(f"InplaceLayer: k/v buffers must be [B,H,L,D] of one shape, got "
-                             f"{tuple(k_buf.shape)} and {tuple(v_buf.shape)}")
-        if not 0 <= base_len <= k_buf.shape[2]:
-            raise ValueError(f"InplaceLayer: base_len {base_len} outside the buffer "
-                             f"({k_buf.shape[2]})")
-        self._k_buf = k_buf
-        self._v_buf = v_buf
-        self._pos = base_len
-        self.keys = k_buf[:, :, :base_len, :]
-        self.values = v_buf[:, :, :base_len, :]
-        self.dtype, self.device = k_buf.dtype, k_buf.device
-        self.is_initialized = True
-        # the buffers never change: check once whether the fused append can
-        # write them, per call only the inputs (a missing library then raises
-        # at the launch, as every fused path does)
-        self._fused_ok = rope.kv_cache_ok(k_buf, v_buf)
-        # Graph mode (set by a decode-graph runner): single-token writes go to
-        # the device position _pos_t, and the first _graph_len rows are
-        # returned, so every replay sees one static shape.
-        self.graph_mode = False
-        self._pos_t: torch.Tensor | None = None
-        self._graph_len = 0
+    def __init__(self, layers: int, batch: int, heads: int, capacity: int, head_dim: int,
+                 dtype: torch.dtype, device: torch.device | str) -> None:
+        if min(layers, batch, heads, head_dim) <= 0 or capacity < 0:
+            raise ValueError(f"KVArena: bad geometry layers={layers} batch={batch} "
+                             f"heads={heads} capacity={capacity} head_dim={head_dim}")
+        self.storage = torch.empty(layers, 2, batch, heads, capacity, head_dim, dtype=dtype,
+                                   device=device)
+        self.fill = [0] * layers
+        self.cursor: torch.Tensor | None = None
+        self.window = 0
+        # the buffers never move: check once whether the fused append can write them
+        self.fused_ok = rope.kv_cache_ok(self.k(0), self.v(0))
 
     @property
     def capacity(self) -> int:
-        return self._k_buf.shape[2]
+        return self.storage.shape[4]
 
-    def _graph_write(self, n: int) -> bool:
-        return self.graph_mode and n == 1 and self._pos_t is not None
+    @property
+    def layers(self) -> int:
+        return self.storage.shape[0]
 
-    def _graph_views(self) -> tuple[torch.Tensor, torch.Tensor]:
-        self.keys = self._k_buf[:, :, :self._graph_len, :].contiguous()
-        self.values = self._v_buf[:, :, :self._graph_len, :].contiguous()
-        return self.keys, self.values
+    def k(self, i: int) -> torch.Tensor:
+        return self.storage[i, 0]
 
-    def _advance(self, n: int) -> tuple[torch.Tensor, torch.Tensor]:
-        self._pos += n
-        self.keys = self._k_buf[:, :, :self._pos, :]
-        self.values = self._v_buf[:, :, :self._pos, :]
-        if n == 1:
-            # single-token steps hand attention contiguous KV (the reference
-            # measured strided views slower for the decode GEMV/flash path)
-            return self.keys.contiguous(), self.values.contiguous()
-        return self.keys, self.values
+    def v(self, i: int) -> torch.Tensor:
+        return self.storage[i, 1]
 
-    def _check_room(self, n: int) -> None:
-        if self._pos + n > self.capacity:
-            raise RuntimeError(f"InplaceLayer overflow: pos {self._pos} + new {n} > "
-                               f"buffer {self.capacity}")
+    def rows(self, i: int, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Views of layer i's first n rows."""
+        return self.storage[i, 0, :, :, :n], self.storage[i, 1, :, :, :n]
+
+    def room(self, i: int, n: int) -> int:
+        """Row where n new tokens of layer i go; raises if they do not fit."""
+        start = self.fill[i]
+        if start + n > self.capacity:
+            raise RuntimeError(f"KV arena overflow (layer {i}): {start} tokens held + {n} new "
+                               f"> capacity {self.capacity}")
+        return start
+
+    def replaying(self, n: int) -> bool:
+        return self.cursor is not None and n == 1
+
+
+class InplaceLayer(DynamicLayer):
+    """Layer ``index`` of an arena with transformers' DynamicLayer interface.
+
+    ``keys`` / ``values`` are refreshed after every operation: views of the
+    valid rows, contiguous copies for single-token steps and replays.
+    """
+
+    def __init__(self, arena: KVArena, index: int) -> None:
+        super().__init__()
+        self.arena, self.index = arena, index
+        self.dtype, self.device = arena.storage.dtype, arena.storage.device
+        self.is_initialized = True
+        self._views()
+
+    @property
+    def capacity(self) -> int:
+        return self.arena.capacity
+
+    def _views(self, n: int | None = None, copy: bool = False):
+        n = self.arena.fill[self.index] if n is None else n
+        k, v = self.arena.rows(self.index, n)
+        if copy:
+            k, v = k.contiguous(), v.contiguous()
+        self.keys, self.values = k, v
+        return k, v
+
+    def _wrote(self, n: int):
+        """Bookkeeping after writing n tokens: the new views."""
+        ar = self.arena
+        if ar.replaying(n):
+            return self._views(ar.window, copy=True)
+        ar.fill[self.index] += n
+        # single-token steps hand attention contiguous KV (the reference
+        # measured strided views slower for the decode attention kernels)
+        return self._views(copy=n == 1)
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
-        """Append already-rotated keys and values (src/umic/cache.py:50-80)."""
-        n = key_states.shape[2]
-        if self._graph_write(n):
-            self._k_buf.index_copy_(2, self._pos_t, key_states)
-            self._v_buf.index_copy_(2, self._pos_t, value_states)
-            return self._graph_views()
-        self._check_room(n)
-        self._k_buf[:, :, self._pos:self._pos + n, :] = key_states
-        self._v_buf[:, :, self._pos:self._pos + n, :] = value_states
-        return self._advance(n)
+        """Append already-rotated keys and their values (src/umic/cache.py:50-80)."""
+        ar, i, n = self.arena, self.index, key_states.shape[2]
+        if ar.replaying(n):
+            ar.k(i).index_copy_(2, ar.cursor, key_states)
+            ar.v(i).index_copy_(2, ar.cursor, value_states)
+        else:
+            r0 = ar.room(i, n)
+            ar.k(i)[:, :, r0:r0 + n] = key_states
+            ar.v(i)[:, :, r0:r0 + n] = value_states
+        return self._wrote(n)
 
     def can_append_rotary(self, q, k, v, cos, sin, norm=None) -> bool:
         """True when ``append_rotary`` takes its one-launch fused path."""
-        return (self._fused_ok and rope.kv_inputs_ok(q, k, v, cos, sin, self._k_buf)
-                and (norm is None or rope.norm_weights_ok(q, norm[0], norm[1])))
+        ar = self.arena
+        if not (ar.fused_ok and rope.kv_inputs_ok(q, k, v, cos, sin, ar.k(self.index))):
+            return False
+        if norm is not None and not rope.norm_weights_ok(q, norm[0], norm[1]):
+            return False
+        if ar.replaying(k.shape[2]):
+            c = ar.cursor
+            return c.dtype == torch.int64 and c.device == self.device
+        return True
 
     def append_rotary(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       cos: torch.Tensor, sin: torch.Tensor, norm=None):
-        """rope(q), and the cache after appending rope(k) and v, in one launch.
-
-        Equivalent to ``apply_rotary_pos_emb(q, k, cos, sin)`` followed by
-        ``update(k_rot, v)`` (bit for bit: the kernel's rotation is the eager
-        bf16 chain's); returns ``(q_rot, keys, values)`` with ``update``'s
-        return conventions, or None -- nothing done -- when the inputs are not
-        a layout the kernel takes (``can_append_rotary``).  With
-        ``norm = (q_w, k_w, eps)``, q and k are the raw projections and the
-        attention's per-head RMSNorms (HF q_norm / k_norm) run first, in the
-        same launch.
-        """
+        """rope(q), and the layer's keys and values after appending rope(k) and
+        v, in one launch: ``(q_rot, keys, values)`` with ``update``'s return
+        conventions, or None -- nothing done -- for inputs the kernel does not
+        take.  Bit for bit ``apply_rotary_pos_emb(q, k, cos, sin)`` followed by
+        ``update``.  With ``norm = (q_w, k_w, eps)`` q and k are the raw
+        projections and the attention's q_norm / k_norm run first, in the
+        same launch."""
         if not self.can_append_rotary(q, k, v, cos, sin, norm):
             return None
-        n = k.shape[2]
-        if self._graph_write(n):
-            if not (self._pos_t.dtype == torch.int64 and self._pos_t.device == self.device):
-                return None
-            q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, 0, self._pos_t,
+        ar, i, n = self.arena, self.index, k.shape[2]
+        if ar.replaying(n):
+            q_rot = rope.kv_launch(q, k, v, cos, sin, ar.k(i), ar.v(i), 0, ar.cursor, norm)
+        else:
+            q_rot = rope.kv_launch(q, k, v, cos, sin, ar.k(i), ar.v(i), ar.room(i, n), None,
                                    norm)
-            return (q_rot, *self._graph_views())
-        self._check_room(n)
-        q_rot = rope.kv_launch(q, k, v, cos, sin, self._k_buf, self._v_buf, self._pos, None, norm)
-        return (q_rot, *self._advance(n))
+        return (q_rot, *self._wrote(n))
 
     def get_seq_length(self, cache_position=None) -> int:
-        return self._pos
+        return self.arena.fill[self.index]
 
     def get_max_length(self) -> int:
-        return self.capacity
+        return self.arena.capacity
 
     def crop(self, max_length: int) -> None:
-        """O(1): move the write pointer back (negative = drop that many)."""
-        if max_length < 0:
-            max_length = self._pos + max_length
-        self._pos = max(0, min(self._pos, max_length))
-        self.keys = self._k_buf[:, :, :self._pos, :]
-        self.values = self._v_buf[:, :, :self._pos, :]
+        """O(1): keep max_length tokens (a negative value drops that many)."""
+        held = self.arena.fill[self.index]
+        keep = held + max_length if max_length < 0 else max_length
+        self.arena.fill[self.index] = max(0, min(held, keep))
+        self._views()
 
 
 class InplaceKVCache(DynamicCache):
-    """DynamicCache whose layers are pre-allocated ``InplaceLayer`` s.
-
-    Subclassing DynamicCache keeps transformers' mask and attention back-end
-    selection identical (src/umic/cache.py:94-160).
-    """
+    """A DynamicCache whose layers are views of ``KVArena`` s."""
 
     def __init__(self, layers: list[InplaceLayer]) -> None:
         super().__init__()
         self.layers = layers
+        self.arenas = list({id(lyr.arena): lyr.arena for lyr in layers}.values())
 
     @classmethod
     def from_dynamic(cls, cache: DynamicCache, extra_tokens: int,
                      margin: int = 8) -> "InplaceKVCache":
-        """Convert once: allocate base_len + extra_tokens + margin rows per
-        layer and copy the existing prefix (src/umic/cache.py:104-128)."""
+        """Copy a populated cache into an arena with room for extra_tokens
+        (+ margin) more tokens per layer.  Layers of one geometry share one
+        arena; any other layer gets its own."""
         layers: list[InplaceLayer] = []
-        alloc = 0
-        for lyr in cache.layers:
-            k, v = lyr.keys, lyr.values
-            b, h, base_len, d = k.shape
-            kb = torch.empty(b, h, base_len + extra_tokens + margin, d, device=k.device,
-                             dtype=k.dtype)
-            vb = torch.empty_like(kb)
-            kb[:, :, :base_len, :] = k
-            vb[:, :, :base_len, :] = v
-            layers.append(InplaceLayer(kb, vb, base_len))
-            alloc += kb.numel() * kb.element_size() * 2
-        logger.info("InplaceKVCache: %d layers converted, base_len=%d, alloc=%.0f MB",
-                    len(layers), layers[0]._pos if layers else 0, alloc / 1e6)
+        arenas: dict[tuple, tuple[KVArena, list[int]]] = {}
+        for idx, lyr in enumerate(cache.layers):
+            k = lyr.keys
+            key = (tuple(k.shape[:2]), k.shape[3], k.shape[2], k.dtype, str(k.device))
+            arenas.setdefault(key, (None, []))[1].append(idx)
+        slot: dict[int, tuple[KVArena, int]] = {}
+        for (bh, d, held, dt, dev), (_, members) in arenas.items():
+            ar = KVArena(len(members), bh[0], bh[1], held + extra_tokens + margin, d, dt, dev)
+            for j, idx in enumerate(members):
+                src = cache.layers[idx]
+                ar.storage[j, 0, :, :, :held].copy_(src.keys)
+                ar.storage[j, 1, :, :, :held].copy_(src.values)
+                ar.fill[j] = held
+                slot[idx] = (ar, j)
+        for idx in range(len(cache.layers)):
+            layers.append(InplaceLayer(*slot[idx]))
         return cls(layers)
+
+    def reseed(self, cache: DynamicCache) -> None:
+        """Copy another cache's contents (same geometry, at most the capacity)
+        into these buffers, in place: captured graphs keep valid addresses."""
+        for dst, src in zip(self.layers, cache.layers):
+            n = src.keys.shape[2]
+            k, v = dst.arena.rows(dst.index, n)
+            k.copy_(src.keys)
+            v.copy_(src.values)
+            dst.arena.fill[dst.index] = n
+            dst._views()
 
     def crop(self, max_length: int) -> None:
         for lyr in self.layers:
             lyr.crop(max_length)
 
-    # --- graph-mode plumbing (driven by a decode-graph runner) -------------
+    # -- graph replay --------------------------------------------------------
 
-    def enable_graph_mode(self, pos_t: torch.Tensor) -> None:
-        """Static-shape decode: writes at device position pos_t, full reads."""
-        for lyr in self.layers:
-            lyr.graph_mode = True
-            lyr._pos_t = pos_t
+    def replay_at(self, cursor: torch.Tensor, window: int) -> None:
+        """Single-token writes go to device row ``cursor``; attention sees
+        ``window`` rows (the KV length the replayed graph was captured at)."""
+        for ar in self.arenas:
+            ar.cursor, ar.window = cursor, window
 
-    def disable_graph_mode(self) -> None:
+    def end_replay(self) -> None:
+        """Back to host-positioned writes at each layer's fill level."""
+        for ar in self.arenas:
+            ar.cursor = None
         for lyr in self.layers:
-            lyr.graph_mode = False
-            lyr.keys = lyr._k_buf[:, :, :lyr._pos, :]
-            lyr.values = lyr._v_buf[:, :, :lyr._pos, :]
+            lyr._views()
 
-    def set_pos(self, n: int) -> None:
-        """Sync the host write pointer after graph replays."""
+    def set_length(self, n: int) -> None:
+        """Every layer holds n tokens (after replays wrote them on the device)."""
         for lyr in self.layers:
-            lyr._pos = n
-
-    def set_graph_len(self, n: int) -> None:
-        """Exact KV length for the graph being captured / replayed."""
-        for lyr in self.layers:
-            lyr._graph_len = n
+            lyr.arena.fill[lyr.index] = n
+            if lyr.arena.cursor is None:
+                lyr._views()
 
     def get_seq_length(self, layer_idx: int = 0, cache_position=None) -> int:
         if layer_idx >= len(self.layers):

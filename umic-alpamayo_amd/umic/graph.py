@@ -1,40 +1,30 @@
-"""Decode-step and flow-step HIP graphs.
+"""HIP graphs for the two repeated steps of a UMIC inference: generate()'s
+single-token decode and the flow expert's ODE step.
 
-``DecodeGraphRunner``: one captured graph per KV length, replayed.
-``FlowStepGraph`` / ``fuse_flow_graph``: one graph for the fixed-shape flow
-ODE step (see their docstrings).
+Both replay captured work on static buffers; what differs is the key.
 
-Same contract as the reference's decode runner (src/umic/graph.py:36-176):
-the runner wraps the VLM's ``forward`` (instance attribute, so module hooks
-still fire) and, during ``generate()``, serves every single-token decode step
-from a graph captured once per KV length.  The graphs persist across
-inferences: the KV buffers, static inputs and M-RoPE delta live in the
-runner, and each new inference copies its prefill KV into them, so captured
-graphs keep valid buffer addresses and later inferences are pure replay.
-Exact-length graphs keep ``attention_mask=None``, which lets attention use
-its fused kernels with grouped-query heads.
+* Decode (``DecodeGraphRunner``): one graph per KV length.  Attention over
+  an exact-length cache keeps attention_mask=None and so the fused SDPA
+  kernels with grouped-query heads; a padded single graph would need a 4-D
+  mask (the reference measured that slower, src/umic/graph.py:11-14).  The
+  runner owns a persistent ``InplaceKVCache``: a new inference with the same
+  prompt length is re-seeded into the same buffers, so graphs captured
+  earlier stay valid and later inferences are pure replay.  Every replay
+  writes its KV row at the arena's device cursor; with
+  ``umic.integrate.fuse_kv_rope`` each layer's q_norm, k_norm, RoPE and append
+  inside the graph is one ``umic_qk_rmsnorm_rope_kv_append_bf16`` launch.
+* Flow (``FlowStepGraph``): the ODE step runs on fixed shapes -- its action
+  tokens are appended to the prefix cache at the same rows and cropped back
+  -- so one graph serves every step; only the values of x and t change.
 
-On this runtime the cache is ``umic.cache.InplaceKVCache`` in graph mode:
-the write position is a device tensor updated before each replay.  With
-``umic.integrate.fuse_kv_rope`` applied, every layer's RoPE and KV write
-inside the graph is one ``umic_rope_kv_append_bf16`` launch reading that
-position (the reference replays RoPE plus two ``index_copy_`` per layer).
-
-Positions.  The installed forward keeps the model's signature, because
-``generate()`` picks the inputs it passes by that signature (transformers 5.x
-passes ``position_ids`` -- [4, B, 1] text + M-RoPE rows -- and no
-``cache_position``).  Each step copies the given position ids into a static
-device buffer that the graph reads; the KV write position is the cache length
-the runner tracks on the host (no device sync).  Without given position ids
-the graph computes them as position + the model's ``rope_deltas`` (the
-reference's rule, src/umic/graph.py:128-136).
+Capture never decides results: a step that cannot be captured runs eagerly.
 """
 
 from __future__ import annotations
 
 import functools
 import logging
-from typing import Any
+from typing import Any, Callable
 
 import torch
 from transformers.cache_utils import DynamicCache
@@ -43,195 +33,251 @@ from umic.cache import InplaceKVCache
 
 logger = logging.getLogger(__name__)
 
-# forward() arguments that carry a new multimodal input or replace input_ids:
-# such a call is not a plain decode step
-_NOT_DECODE = ("inputs_embeds", "pixel_values", "pixel_values_videos")
-# arguments the static call supplies itself
-_STATIC = ("input_ids", "attention_mask", "past_key_values", "position_ids", "cache_position")
+
+def _on_side_stream(fn: Callable[[], Any]):
+    """Run fn on a side stream ordered after the current one (allocator and
+    library lazy initialisation must not land inside a later capture: the
+    torch.cuda.graphs warm-up recipe)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = fn()
+    torch.cuda.current_stream().wait_stream(side)
+    return out
+
+
+def _capture(fn: Callable[[], Any], pool=None, warm: bool = True):
+    """Capture one call of fn in a new graph, after one warm-up call on a
+    side stream unless ``warm`` is False; returns (graph, outputs)."""
+    if warm:
+        _on_side_stream(fn)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, pool=pool):
+        out = fn()
+    return graph, out
+
+
+class _GraphBank:
+    """Captured steps keyed by KV length, sharing one memory pool."""
+
+    def __init__(self) -> None:
+        self._steps: dict[int, tuple[torch.cuda.CUDAGraph, Any]] = {}
+        self._pool = None
+
+    def __len__(self) -> int:
+        return len(self._steps)
+
+    def __contains__(self, key: int) -> bool:
+        return key in self._steps
+
+    def run(self, key: int, fn: Callable[[], Any], warm: bool):
+        """Replay the step for key, capturing it first if needed; its outputs."""
+        if key not in self._steps:
+            graph, out = _capture(fn, self._pool, warm)
+            if self._pool is None:
+                self._pool = graph.pool()
+            self._steps[key] = (graph, out)
+        graph, out = self._steps[key]
+        graph.replay()
+        return out
+
+    def clear(self) -> None:
+        self._steps.clear()
+        self._pool = None
+
+
+class _StepIO:
+    """Static device inputs of the captured decode step: the token, the
+    position ids (the form generate() passes, or None), the model's M-RoPE
+    delta and the arena write cursor."""
+
+    def __init__(self, device, pids: torch.Tensor | None) -> None:
+        self.ids = torch.zeros(1, 1, dtype=torch.long, device=device)
+        self.cursor = torch.zeros(1, dtype=torch.long, device=device)
+        self.delta = torch.zeros(1, dtype=torch.long, device=device)
+        self.pids = None if pids is None else torch.zeros_like(pids)
+
+    def matches(self, pids: torch.Tensor | None) -> bool:
+        if (pids is None) != (self.pids is None):
+            return False
+        return pids is None or (pids.shape == self.pids.shape and pids.dtype == self.pids.dtype)
+
+    def load(self, ids: torch.Tensor, pids: torch.Tensor | None, pos: int) -> None:
+        self.ids.copy_(ids)
+        self.cursor.fill_(pos)
+        if pids is not None:
+            self.pids.copy_(pids)
+
+    def position_ids(self) -> torch.Tensor:
+        if self.pids is not None:
+            return self.pids
+        # no ids given: text position + the model's rope delta on all three
+        # M-RoPE rows (src/umic/graph.py:128-136)
+        return (self.cursor + self.delta).view(1, 1, 1).expand(3, 1, 1)
+
+
+# forward() arguments that carry new multimodal input or replace input_ids
+_MULTIMODAL = ("inputs_embeds", "pixel_values", "pixel_values_videos")
+# arguments the captured step supplies itself
+_STEP_ARGS = ("input_ids", "attention_mask", "past_key_values", "position_ids", "cache_position")
 
 
 class DecodeGraphRunner:
-    """Wraps a VLM's forward; replays per-KV-length graphs for decode."""
+    """Installs itself as the VLM's forward and serves generate()'s
+    single-token decode steps from per-KV-length graphs (public contract of
+    src/umic/graph.py:36-176: persistent buffers, a re-seed per inference,
+    sampling left eager between replays).  Every other call -- prefill,
+    multimodal input, padded prompts, CPU tensors -- runs the model's own
+    forward."""
 
     def __init__(self, vlm: torch.nn.Module, max_new_tokens: int = 96,
                  warmup_steps: int = 2) -> None:
         self.vlm = vlm
-        self.orig_forward = vlm.forward
         self.max_new = max_new_tokens
         self.warmup_steps = warmup_steps
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.outs: dict[int, Any] = {}
-        self.pool = None
-        self.cache: InplaceKVCache | None = None   # persistent KV buffers
-        self.base_len: int | None = None
-        self.in_decode = False
-        self.disabled = False
-        self.step = 0
         self.replays = 0
-        self.s_ids = self.s_pos = self.s_rope = self.s_pids = None
-        self.static_kwargs: dict[str, Any] = {}
+        self._model_forward = vlm.forward
+        self._bank = _GraphBank()
+        self._kv: InplaceKVCache | None = None     # persistent arena cache
+        self._kv_prompt: int | None = None         # prompt length it was built for
+        self._io: _StepIO | None = None
+        self._step_kwargs: dict[str, Any] = {}
+        self._eager_steps = 0
+        self._live = False                          # inside a decode session on _kv
+        self._off = False                           # a capture failed: eager for good
 
-        @functools.wraps(self.orig_forward)
+        @functools.wraps(self._model_forward)
         def forward(*args: Any, **kwargs: Any):
-            return self(*args, **kwargs)
+            return self._dispatch(args, kwargs)
 
         forward._umic_runner = self
         vlm.forward = forward
-        orig_generate = getattr(vlm, "generate", None)
-        if orig_generate is not None:
-            def _generate(*args: Any, **kwargs: Any):
+        generate = getattr(vlm, "generate", None)
+        if generate is not None:
+            @functools.wraps(generate)
+            def generate_and_release(*args: Any, **kwargs: Any):
                 try:
-                    return orig_generate(*args, **kwargs)
+                    return generate(*args, **kwargs)
                 finally:
-                    self.finish()
+                    self._close()
 
-            vlm.generate = _generate
-        logger.info("DecodeGraphRunner installed on %s", type(vlm).__name__)
+            vlm.generate = generate_and_release
+        logger.info("decode graph runner installed on %s", type(vlm).__name__)
 
-    # -- inference boundaries ----------------------------------------------
+    # public views of the runner's state
+    @property
+    def graphs(self) -> _GraphBank:
+        return self._bank
 
-    def finish(self) -> None:
-        """generate() returned: leave the cache in dynamic mode."""
-        if self.cache is not None:
-            self.cache.disable_graph_mode()
-        self.in_decode = False
-        self.step = 0
+    @property
+    def cache(self) -> InplaceKVCache | None:
+        return self._kv
 
-    def _is_decode_call(self, args, kwargs) -> bool:
-        ids = kwargs.get("input_ids")
-        pkv = kwargs.get("past_key_values")
-        return (not args and not self.disabled and isinstance(ids, torch.Tensor)
-                and ids.is_cuda and tuple(ids.shape) == (1, 1)
-                and isinstance(pkv, DynamicCache) and pkv.get_seq_length() > 0
-                and all(kwargs.get(k) is None for k in _NOT_DECODE)
+    @property
+    def wrapped_forward(self):
+        """The model forward the runner dispatches to."""
+        return self._model_forward
+
+    # -- session bookkeeping -----------------------------------------------
+
+    def _close(self) -> None:
+        """A generate() returned (or a step went eager): host-positioned writes
+        again, so the cache is an ordinary in-place cache for later users."""
+        if self._kv is not None:
+            self._kv.end_replay()
+        self._live = False
+        self._eager_steps = 0
+
+    def _is_step(self, args, kwargs) -> bool:
+        ids, pkv = kwargs.get("input_ids"), kwargs.get("past_key_values")
+        return (not args and not self._off and isinstance(ids, torch.Tensor) and ids.is_cuda
+                and tuple(ids.shape) == (1, 1) and isinstance(pkv, DynamicCache)
+                and pkv.get_seq_length() > 0
+                and all(kwargs.get(name) is None for name in _MULTIMODAL)
                 and not torch.cuda.is_current_stream_capturing())
 
-    def _begin_inference(self, kwargs: dict[str, Any]) -> bool:
-        """First decode step of a generate() call: bind the persistent cache."""
+    def _open(self, kwargs: dict[str, Any]) -> bool:
+        """First decode step of a generate(): move its cache into the arena."""
         pkv = kwargs["past_key_values"]
-        if not all(getattr(lyr, "keys", None) is not None for lyr in pkv.layers):
+        if any(getattr(lyr, "keys", None) is None for lyr in pkv.layers):
             return False
         mask = kwargs.get("attention_mask")
         if mask is not None and not bool((mask == 1).all().item()):
-            logger.warning("DecodeGraphRunner: padded attention mask -- eager decode")
+            logger.warning("decode graph runner: padded prompt, decoding eagerly")
             return False
-        base = pkv.get_seq_length()
-        if pkv is self.cache:
-            pass                                   # continuing on our own buffers
-        elif self.cache is not None and base == self.base_len:
-            # same prompt length: copy the new prefill KV into the persistent
-            # buffers, so the captured graphs' addresses stay valid
-            for dst, src in zip(self.cache.layers, pkv.layers):
-                dst._k_buf[:, :, :base].copy_(src.keys)
-                dst._v_buf[:, :, :base].copy_(src.values)
-            self.cache.set_pos(base)
-        else:
-            if self.cache is not None:
-                logger.info("DecodeGraphRunner: prompt length %s -> %d, recapturing",
-                            self.base_len, base)
-                self.graphs.clear()
-                self.outs.clear()
-                self.pool = None
-            self.cache = InplaceKVCache.from_dynamic(pkv, extra_tokens=self.max_new)
-            self.base_len = base
-        dev = kwargs["input_ids"].device
-        if self.s_ids is None:
-            self.s_ids = torch.zeros(1, 1, dtype=torch.long, device=dev)
-            self.s_pos = torch.zeros(1, dtype=torch.long, device=dev)
-            self.s_rope = torch.zeros(1, dtype=torch.long, device=dev)
-        deltas = getattr(getattr(self.vlm, "model", None), "rope_deltas", None)
-        if isinstance(deltas, torch.Tensor):
-            self.s_rope.copy_(deltas.reshape(-1)[:1])
-        else:
-            self.s_rope.zero_()
+        prompt = pkv.get_seq_length()
+        if pkv is not self._kv:
+            if self._kv is not None and prompt == self._kv_prompt:
+                self._kv.reseed(pkv)             # same buffers: graphs stay valid
+            else:
+                if self._kv is not None:
+                    logger.info("decode graph runner: prompt %s -> %d tokens, new graphs",
+                                self._kv_prompt, prompt)
+                self._bank.clear()
+                self._kv = InplaceKVCache.from_dynamic(pkv, extra_tokens=self.max_new)
+                self._kv_prompt = prompt
         pids = kwargs.get("position_ids")
-        shape = None if pids is None else tuple(pids.shape)
-        if (self.s_pids is None) != (pids is None) or (
-                pids is not None and tuple(self.s_pids.shape) != shape):
-            # the static position input changes form: graphs must be recaptured
-            self.graphs.clear()
-            self.outs.clear()
-            self.s_pids = None if pids is None else torch.zeros(shape, dtype=pids.dtype,
-                                                                device=dev)
-        self.cache.enable_graph_mode(self.s_pos)
-        self.static_kwargs = {k: v for k, v in kwargs.items() if k not in _STATIC}
-        self.in_decode = True
+        if self._io is None or not self._io.matches(pids):
+            self._bank.clear()                   # the step's inputs change form
+            self._io = _StepIO(kwargs["input_ids"].device, pids)
+        delta = getattr(getattr(self.vlm, "model", None), "rope_deltas", None)
+        if isinstance(delta, torch.Tensor):
+            self._io.delta.copy_(delta.reshape(-1)[:1])
+        else:
+            self._io.delta.zero_()
+        self._step_kwargs = {k: v for k, v in kwargs.items() if k not in _STEP_ARGS}
+        self._live = True
         return True
 
-    # -- the captured step ---------------------------------------------------
+    # -- the step ----------------------------------------------------------
 
-    def _static_call(self):
-        pos = self.s_pids
-        if pos is None:
-            pos = (self.s_pos + self.s_rope).view(1, 1, 1).expand(3, 1, 1)
-        return self.orig_forward(input_ids=self.s_ids, attention_mask=None,
-                                 past_key_values=self.cache, position_ids=pos,
-                                 **self.static_kwargs)
+    def _static_step(self):
+        io = self._io
+        return self._model_forward(input_ids=io.ids, attention_mask=None,
+                                   past_key_values=self._kv, position_ids=io.position_ids(),
+                                   **self._step_kwargs)
 
     def _eager(self, args, kwargs):
-        """Run the step eagerly.  A step on the runner's cache leaves graph
-        mode first, so it appends at the host-side position."""
-        if self.in_decode and kwargs.get("past_key_values") is self.cache:
-            self.finish()
-        return self.orig_forward(*args, **kwargs)
+        if self._live and kwargs.get("past_key_values") is self._kv:
+            self._close()                        # appends at the host position
+        return self._model_forward(*args, **kwargs)
 
-    def __call__(self, *args: Any, **kwargs: Any):
-        if not self._is_decode_call(args, kwargs):
+    def _dispatch(self, args, kwargs):
+        if not self._is_step(args, kwargs):
             return self._eager(args, kwargs)
-        pkv = kwargs["past_key_values"]
-        if (not self.in_decode or pkv is not self.cache) and not self._begin_inference(kwargs):
+        if (not self._live or kwargs["past_key_values"] is not self._kv) and \
+                not self._open(kwargs):
             return self._eager(args, kwargs)
-        pos = self.cache.get_seq_length()           # tokens already cached (host)
-        if pos + 1 > self.cache.layers[0].capacity:
-            raise RuntimeError(f"DecodeGraphRunner: decode step {pos + 1 - self.base_len} "
-                               f"exceeds the cache headroom (max_new_tokens={self.max_new})")
-        kv_len = pos + 1
-        pids = kwargs.get("position_ids")
-        if (pids is None) != (self.s_pids is None) or (
-                pids is not None and pids.shape != self.s_pids.shape):
-            return self._eager(args, kwargs)             # not the captured form
-        self.s_ids.copy_(kwargs["input_ids"])
-        self.s_pos.fill_(pos)
-        if pids is not None:
-            self.s_pids.copy_(pids)
-        self.cache.set_graph_len(kv_len)
-        if not self.graphs and self.step < self.warmup_steps:
-            # lazy library initialisation runs before the first capture
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                out = self._static_call()
-            torch.cuda.current_stream().wait_stream(side)
-        elif kv_len not in self.graphs:
-            try:
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, pool=self.pool):
-                    self.outs[kv_len] = self._static_call()
-            except Exception as exc:  # noqa: BLE001 -- correctness first
-                logger.warning("DecodeGraphRunner: capture failed (%s); eager decode", exc)
-                self.disabled = True
-                self.cache.set_pos(pos)
-                return self._eager(args, kwargs)
-            if self.pool is None:
-                self.pool = graph.pool()
-            self.graphs[kv_len] = graph
-            graph.replay()
-            self.replays += 1
-            out = self.outs[kv_len]
+        if not self._io.matches(kwargs.get("position_ids")):
+            return self._eager(args, kwargs)
+        pos = self._kv.get_seq_length()          # tokens held (host)
+        if pos + 1 > self._kv.layers[0].capacity:
+            raise RuntimeError(f"decode graph runner: step {pos + 1 - self._kv_prompt} is past "
+                               f"the cache headroom (max_new_tokens={self.max_new})")
+        self._io.load(kwargs["input_ids"], kwargs.get("position_ids"), pos)
+        self._kv.replay_at(self._io.cursor, pos + 1)
+        if not len(self._bank) and self._eager_steps < self.warmup_steps:
+            # the first steps of a runner's life run the static step eagerly
+            # (library lazy initialisation happens outside any capture)
+            self._eager_steps += 1
+            out = _on_side_stream(self._static_step)
         else:
-            self.graphs[kv_len].replay()
+            try:
+                out = self._bank.run(pos + 1, self._static_step, warm=False)
+            except Exception as exc:  # noqa: BLE001 -- results never depend on capture
+                logger.warning("decode graph runner: capture failed (%s), decoding eagerly", exc)
+                self._off = True
+                self._kv.set_length(pos)
+                return self._eager(args, kwargs)
             self.replays += 1
-            out = self.outs[kv_len]
-        self.step += 1
-        self.cache.set_pos(kv_len)
+        self._kv.set_length(pos + 1)
         return out
 
 
 def fuse_decode_graph(vlm: torch.nn.Module, max_new_tokens: int = 96) -> DecodeGraphRunner:
     """Install the per-length decode graph runner on the VLM
     (src/umic/graph.py:179-181).  Idempotent: a VLM that already carries a
-    runner keeps it (a second one would wrap the first and keep a second KV
-    cache)."""
+    runner keeps it, with the larger headroom."""
     existing = getattr(getattr(vlm, "forward", None), "_umic_runner", None)
     if isinstance(existing, DecodeGraphRunner):
         existing.max_new = max(existing.max_new, max_new_tokens)
@@ -240,70 +286,66 @@ def fuse_decode_graph(vlm: torch.nn.Module, max_new_tokens: int = 96) -> DecodeG
 
 
 class FlowStepGraph:
-    """One captured graph for a fixed-shape flow ODE step, replayed per step.
-
-    Same contract as src/umic/graph.py:179-232.  Every step of the flow
-    expert runs ``step_fn(x=, t=)`` on the same shapes: its action tokens are
-    appended to the prefix KV at the same cache rows and cropped back, so the
-    buffers the kernels touch are identical each step and only the values of
-    x and t change.  After ``warmup`` eager steps the step is captured once
-    (on static copies of x and t); later steps copy x and t in and replay.
-    With ``umic.integrate.fuse_kv_rope`` the attention's RoPE and cache write
-    inside the graph is one launch at the baked cache position.  A capture
-    that fails falls back to eager for good, so results never depend on it.
-    The graph holds the buffer addresses of the cache it was captured on:
-    build a new one per inference (per prompt cache).
-    """
+    """``step_fn(x=, t=)`` served from one graph after ``warmup`` eager calls
+    (contract of src/umic/graph.py:179-232).  The graph holds the addresses of
+    the cache it was captured on: one instance per inference."""
 
     def __init__(self, step_fn, warmup: int = 2) -> None:
         self.step_fn = step_fn
         self.warmup = warmup
-        self.n = 0
-        self.graph: torch.cuda.CUDAGraph | None = None
-        self.xs: torch.Tensor | None = None
-        self.ts: torch.Tensor | None = None
-        self.out: torch.Tensor | None = None
-        self.failed = False
+        self.calls = 0
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self._xt: tuple[torch.Tensor, torch.Tensor] | None = None
+        self._out: torch.Tensor | None = None
+        self._off = False
+
+    @property
+    def captured(self) -> bool:
+        return self._graph is not None
+
+    @property
+    def disabled(self) -> bool:
+        """A capture failed: every later step runs eagerly."""
+        return self._off
+
+    def _try_capture(self, x: torch.Tensor, t: torch.Tensor) -> bool:
+        xs, ts = x.clone(), t.clone()
+        try:
+            graph, out = _capture(lambda: self.step_fn(x=xs, t=ts))
+        except Exception as exc:  # noqa: BLE001 -- results never depend on capture
+            logger.warning("flow step graph: capture failed (%s), eager steps", exc)
+            self._off = True
+            return False
+        self._graph, self._xt, self._out = graph, (xs, ts), out
+        logger.info("flow step graph captured at call %d", self.calls)
+        return True
 
     def __call__(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
-        if self.failed or (self.graph is None and self.n < self.warmup):
-            self.n += 1
+        self.calls += 1
+        if self._graph is None and (self._off or self.calls <= self.warmup
+                                    or not self._try_capture(x, t)):
             return self.step_fn(x=x, t=t)
-        if self.graph is None:
-            try:
-                self.xs, self.ts = x.clone(), t.clone()
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(side):
-                    self.step_fn(x=self.xs, t=self.ts)
-                torch.cuda.current_stream().wait_stream(side)
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    self.out = self.step_fn(x=self.xs, t=self.ts)
-                self.graph = graph
-                logger.info("FlowStepGraph captured (step %d)", self.n)
-            except Exception as exc:  # noqa: BLE001 -- correctness first
-                logger.warning("FlowStepGraph: capture failed (%s); eager steps", exc)
-                self.failed = True
-                return self.step_fn(x=x, t=t)
-        self.n += 1
-        self.xs.copy_(x)
-        self.ts.copy_(t)
-        self.graph.replay()
-        return self.out.clone()
+        self._xt[0].copy_(x)
+        self._xt[1].copy_(t)
+        self._graph.replay()
+        return self._out.clone()
+
+
+_FLOW_STEP_KWARGS = ("step_fn", "unguided_step_fn")
 
 
 def fuse_flow_graph(model: torch.nn.Module, warmup: int = 2) -> None:
-    """Wrap the step closures ``model.diffusion.sample`` receives in
-    ``FlowStepGraph`` (src/umic/graph.py:235-253); nothing else changes."""
-    diffusion = model.diffusion
-    orig_sample = diffusion.sample
+    """Serve the flow expert's ODE steps from graphs: the step closures that
+    ``model.diffusion.sample`` receives are wrapped in ``FlowStepGraph``
+    (src/umic/graph.py:235-253)."""
+    sample = model.diffusion.sample
 
-    def sample(*args, **kwargs):
-        for key in ("step_fn", "unguided_step_fn"):
-            if kwargs.get(key) is not None:
-                kwargs[key] = FlowStepGraph(kwargs[key], warmup)
-        return orig_sample(*args, **kwargs)
+    @functools.wraps(sample)
+    def sample_with_graphs(*args, **kwargs):
+        for name in _FLOW_STEP_KWARGS:
+            if kwargs.get(name) is not None:
+                kwargs[name] = FlowStepGraph(kwargs[name], warmup)
+        return sample(*args, **kwargs)
 
-    diffusion.sample = sample
-    logger.info("fuse_flow_graph: flow ODE step graph runner installed")
+    model.diffusion.sample = sample_with_graphs
+    logger.info("fuse_flow_graph: flow ODE step graphs installed")

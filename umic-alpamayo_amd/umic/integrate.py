@@ -55,9 +55,20 @@ def _gemm_rows_ok(x: torch.Tensor) -> bool:
     return rows >= FUSE_MIN_ROWS or 1 <= rows <= GEMV_MAX_ROWS
 
 
+def _hooked(*mods) -> bool:
+    """True if calling any of mods would run forward hooks (the module's own
+    or global ones): the decode paths that call kernels in place of a
+    submodule's __call__ then take the module call instead, so hooks fire."""
+    from torch.nn.modules import module as _m
+
+    if _m._global_forward_hooks or _m._global_forward_pre_hooks:
+        return True
+    return any(m is not None and (m._forward_hooks or m._forward_pre_hooks) for m in mods)
+
+
 def _linear(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """mod(x) for an nn.Linear, on the library's GEMV in the decode regime."""
-    if (isinstance(mod, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS
+    if (isinstance(mod, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS and not _hooked(mod)
             and linear.linear_eligible(x, mod.weight, mod.bias)
             and not grad_needed(x, mod.weight, mod.bias)):
         return linear.linear_hip(x, mod.weight, mod.bias)
@@ -263,6 +274,8 @@ def _decode_mlp_residual(mlp: nn.Module, x: torch.Tensor, residual: torch.Tensor
     if getattr(mlp.forward, "__func__", None) is not _fused_mlp_forward:
         return None
     down = getattr(mlp, "down_proj", None)
+    if _hooked(mlp, down):
+        return None
     wg, wu = mlp.gate_proj.weight, mlp.up_proj.weight
     if not (isinstance(down, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS
             and fused_ffn.p5_eligible(x, wg, wu)
@@ -679,6 +692,7 @@ def _qkv(attn: nn.Module, x: torch.Tensor) -> list[torch.Tensor]:
     launch for all three (umic_linear_multi_bf16), else each on its own."""
     mods = (attn.q_proj, attn.k_proj, attn.v_proj)
     if (1 <= _rows(x) <= GEMV_MAX_ROWS and all(isinstance(m, nn.Linear) for m in mods)
+            and not _hooked(*mods)
             and all(linear.linear_eligible(x, m.weight, m.bias) for m in mods)
             and not grad_needed(x, *(m.weight for m in mods), *(m.bias for m in mods))):
         return linear.linear_multi_hip(x, [m.weight for m in mods], [m.bias for m in mods])
@@ -690,7 +704,7 @@ def _head_norms(module: nn.Module, q: torch.Tensor):
     (class name contains "rmsnorm", 1-D weight, one eps) that the fused
     norm + RoPE kernels take for ``q``; else None."""
     qn, kn = getattr(module, "q_norm", None), getattr(module, "k_norm", None)
-    if not all("rmsnorm" in type(n).__name__.lower() for n in (qn, kn)):
+    if not all("rmsnorm" in type(n).__name__.lower() for n in (qn, kn)) or _hooked(qn, kn):
         return None
     qw, kw = getattr(qn, "weight", None), getattr(kn, "weight", None)
     eps = _norm_eps(qn)
