@@ -34,6 +34,7 @@ extern "C" {
 #define UMIC_OK 0
 #define UMIC_ERR_INVALID_ARG (-1)  /* null pointer, negative size, bad enum */
 #define UMIC_ERR_UNSUPPORTED (-2)  /* shape / stride / alignment not handled */
+#define UMIC_ERR_SCRATCH (-3)      /* shape needs more than the static scratch */
 
 /* Library version string, e.g. "umic-hip 0.1.0 gfx950". */
 const char* umic_version(void);
@@ -252,6 +253,29 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
                         int64_t M, int64_t N, int64_t K,
                         int64_t ldx, int64_t ldw, int64_t ldo,
                         int act, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * umic_linear_ws_bf16 without a workspace argument and without allocating:
+ * the stream-K schedule runs on a static device scratch array of the
+ * library (64 MiB per device, held from the library's first use on that
+ * device until the process ends).  Same arguments (minus the workspace),
+ * numerics, shape rules and results as umic_linear_ws_bf16 with a large
+ * enough workspace; shapes the data-parallel kernel or the GEMV serve run
+ * those, as there.  A shape whose stream-K workspace
+ * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 85 output tiles
+ * of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  Each call
+ * clears the scratch's tile counters with a kernel (no memset), then runs
+ * the GEMM.  All calls on one device share its scratch: calls that may
+ * overlap in time on one device (different streams without ordering) race
+ * and give wrong results; calls on one stream are safe.
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation).
+ */
+int umic_linear_sk_static_bf16(const void* x, const void* w, const void* bias, void* out,
+                               int64_t M, int64_t N, int64_t K,
+                               int64_t ldx, int64_t ldw, int64_t ldo,
+                               int act, void* stream);
 
 /*
  * Up to three linears over one x in one launch, the decode GEMV path only:

@@ -38,7 +38,8 @@ def test_header_declares_expected_entry_points():
               "umic_gate_silu_mul_bf16", "umic_linear_workspace_bytes", "umic_linear_ws_bf16",
               "umic_linear_multi_bf16", "umic_linear_add_bf16",
               "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
-              "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_version", "umic_error_string"):
+              "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_linear_sk_static_bf16",
+              "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -68,6 +69,7 @@ def test_version_and_error_strings(lib):
     assert _lib.error_string(0) == "success"
     assert "invalid" in _lib.error_string(_lib.UMIC_ERR_INVALID_ARG)
     assert "unsupported" in _lib.error_string(_lib.UMIC_ERR_UNSUPPORTED)
+    assert "scratch" in _lib.error_string(_lib.UMIC_ERR_SCRATCH)
     assert _lib.error_string(-99) == "unknown umic error"
 
 
@@ -98,6 +100,14 @@ def test_argument_rejection_before_launch(lib):
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 7, None) == E_ARG
     assert lib.umic_linear_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 64, 3, None) == E_ARG
     assert lib.umic_linear_bf16(fake, fake, None, fake, 0, 64, 128, 128, 128, 64, 0, None) == 0
+    # the static-scratch stream-K linear checks its arguments the same way
+    sk = lib.umic_linear_sk_static_bf16
+    assert sk(None, None, None, None, 0, 64, 128, 128, 128, 64, 0, None) == 0
+    assert sk(None, fake, None, fake, 300, 4096, 12288, 12288, 12288, 4096, 0, None) == E_ARG
+    assert sk(fake, fake, None, fake, -1, 64, 128, 128, 128, 64, 0, None) == E_ARG
+    assert sk(fake, fake, None, fake, 300, 4096, 12288, 12288, 12288, 4096, 3, None) == E_ARG
+    assert sk(fake, fake, None, fake, 300, 4092, 12288, 12288, 12288, 4092, 0, None) == E_UNS
+    assert sk(fake, fake, fake + 2, fake, 300, 4096, 12288, 12288, 12288, 4096, 0, None) == E_UNS
     assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
                                        None) == E_ARG
     # stream-K linear: same validation; a negative workspace size is rejected

@@ -44,6 +44,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <mutex>
 
 namespace umic {
 namespace {
@@ -967,6 +968,46 @@ bool gemm_shape_ok(const void* x, const void* w0, const void* w1, const void* ou
   return true;
 }
 
+// ---- Allocation-free stream-K --------------------------------------------
+//
+// umic_linear_sk_static_bf16 runs the stream-K schedule on this file-scope
+// scratch instead of a caller's workspace, for callers that cannot allocate
+// (code under graph capture, serving loops).  Each device holds its own copy
+// for the life of the process.  Host code never passes `scratch` itself --
+// on the host the name is a stand-in, not a device address -- only the
+// per-device address hipGetSymbolAddress returns (scratch_address).
+constexpr int64_t kScratchBytes = (int64_t)64 << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current; 0 or a hipError_t value.
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[kScratchDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kScratchDevices) return UMIC_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return UMIC_ERR_SCRATCH;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return UMIC_OK;
+}
+
+// Zeroes n ints (the stream-K tile counters) with vector stores: a kernel,
+// not a memset, so a captured graph replays it like any other node.
+__global__ __launch_bounds__(256) void zero_ints_kernel(int* p, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) p[i] = 0;
+}
+
 }  // namespace
 }  // namespace umic
 
@@ -999,6 +1040,41 @@ extern "C" int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) 
   return sk_plan(M, N, K).bytes;
 }
 
+namespace umic {
+namespace {
+
+// Argument checks of the stream-K launch (the data-parallel path does its own).
+int sk_args_ok(const void* x, const void* w, const void* bias, const void* out, int64_t M,
+               int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldo, int act) {
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
+    return UMIC_ERR_INVALID_ARG;
+  if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
+  if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
+  if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
+  return UMIC_OK;
+}
+
+// The stream-K launch on workspace ws (>= pl.bytes, 256-byte aligned, zero
+// counters), after sk_args_ok.
+int run_linear_sk(const void* x, const void* w, const void* bias, void* out, int64_t M, int64_t N,
+                  int64_t K, int64_t ldx, int64_t ldw, int64_t ldo, int act, const SkPlan& pl,
+                  void* workspace, hipStream_t st) {
+  GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
+             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0};
+  if (act == UMIC_ACT_GELU)
+    return bias ? launch_gemm_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
+                : launch_gemm_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
+  if (act == UMIC_ACT_GELU_TANH)
+    return bias ? launch_gemm_sk<UMIC_ACT_GELU_TANH, true>(g, pl, workspace, st)
+                : launch_gemm_sk<UMIC_ACT_GELU_TANH, false>(g, pl, workspace, st);
+  return bias ? launch_gemm_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
+              : launch_gemm_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
+}
+
+}  // namespace
+}  // namespace umic
+
 extern "C" int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* out,
                                    int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                                    int64_t ldo, int act, void* workspace,
@@ -1008,23 +1084,36 @@ extern "C" int umic_linear_ws_bf16(const void* x, const void* w, const void* bia
   if (pl.bytes == 0 || workspace_bytes < pl.bytes || !workspace ||
       ((uintptr_t)workspace & 255u))  // data-parallel path
     return umic_linear_bf16(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, stream);
-  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
-    return UMIC_ERR_INVALID_ARG;
-  if (!x || !w || !out) return UMIC_ERR_INVALID_ARG;
-  if (ldx < K || ldw < K || ldo < N) return UMIC_ERR_INVALID_ARG;
-  if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
-  if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
-  GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
-             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0};
+  const int rc = sk_args_ok(x, w, bias, out, M, N, K, ldx, ldw, ldo, act);
+  if (rc != UMIC_OK) return rc;
+  return run_linear_sk(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, pl, workspace,
+                       as_stream(stream));
+}
+
+extern "C" int umic_linear_sk_static_bf16(const void* x, const void* w, const void* bias,
+                                          void* out, int64_t M, int64_t N, int64_t K,
+                                          int64_t ldx, int64_t ldw, int64_t ldo, int act,
+                                          void* stream) {
+  if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return UMIC_OK;  // empty tensors may carry null pointers
+  int rc = sk_args_ok(x, w, bias, out, M, N, K, ldx, ldw, ldo, act);
+  if (rc != UMIC_OK) return rc;
+  const SkPlan pl = sk_plan(M, N, K);
+  if (pl.bytes == 0)  // the data-parallel kernel or the GEMV: no scratch needed
+    return umic_linear_bf16(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, stream);
+  if (pl.bytes > kScratchBytes) return UMIC_ERR_SCRATCH;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != UMIC_OK) return rc;
+  // The counters start at zero on every call, whatever an earlier call on
+  // this device left behind.
   hipStream_t st = as_stream(stream);
-  if (act == UMIC_ACT_GELU)
-    return bias ? launch_gemm_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
-                : launch_gemm_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
-  if (act == UMIC_ACT_GELU_TANH)
-    return bias ? launch_gemm_sk<UMIC_ACT_GELU_TANH, true>(g, pl, workspace, st)
-                : launch_gemm_sk<UMIC_ACT_GELU_TANH, false>(g, pl, workspace, st);
-  return bias ? launch_gemm_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
-              : launch_gemm_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
+  const int n = (int)(2 * pl.tiles);
+  hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     static_cast<int*>(ws), n);
+  rc = launch_status();
+  if (rc != UMIC_OK) return rc;
+  return run_linear_sk(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, pl, ws, st);
 }
 
 extern "C" int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void* wu, void* out,

@@ -25,6 +25,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libu
 UMIC_OK = 0
 UMIC_ERR_INVALID_ARG = -1
 UMIC_ERR_UNSUPPORTED = -2
+UMIC_ERR_SCRATCH = -3
 UMIC_ROPE_TEXT = 0
 UMIC_ROPE_VISION = 1
 UMIC_ACT_NONE = 0
@@ -54,6 +55,7 @@ SIGNATURES: dict[str, list] = {
     "umic_gate_silu_mul_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "umic_linear_workspace_bytes": [_I64, _I64, _I64],
     "umic_linear_ws_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
+    "umic_linear_sk_static_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "umic_version": [],
     "umic_error_string": [_I],
 }
