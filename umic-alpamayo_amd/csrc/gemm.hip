@@ -70,8 +70,6 @@ struct GemmArgs {
   uint16_t* out;
   int64_t M, N, K, ldx, ldw0, ldw1, ldo;
   int tiles_m, tiles;
-  const uint16_t* resid;  // GEMV only: out = bf16(resid + bf16(result)), or NULL
-  int64_t ldr;
 };
 
 // LDS geometry of one operand tile of a K step: a row is BK bf16 = 64 bytes
@@ -704,54 +702,55 @@ __device__ __forceinline__ float gemv_epilogue(float v, float u, float bias) {
   }
 }
 
-// Up to kGemvMaxSegs linears over one x in one launch (the attention's
-// q/k/v projections at decode): segment i owns workgroups [first[i],
-// first[i + 1]) and its own weight, bias, output, N and leading dims.  A
-// single linear (or P5, whose gate/up pair lives in GemmArgs) is one segment.
+// The GEMV kernel's one argument: x, and up to kGemvMaxSegs linears over it
+// in one launch (the attention's q/k/v projections at decode).  Segment i
+// owns workgroups [first[i], first[i + 1]) and has its own weights, bias,
+// output, N and leading dims; a single linear, or P5 with its gate/up pair
+// in w0/w1, is one segment.  Every operand the kernel reads comes from here.
 constexpr int kGemvMaxSegs = 3;
-struct GemvSegs {
-  const uint16_t* w[kGemvMaxSegs];
-  const uint16_t* bias[kGemvMaxSegs];
-  uint16_t* out[kGemvMaxSegs];
-  int64_t N[kGemvMaxSegs], ldw[kGemvMaxSegs], ldo[kGemvMaxSegs];
+struct GemvSeg {
+  const uint16_t* w0;    // linear weight, or P5's gate weight
+  const uint16_t* w1;    // P5's up weight (read only when NB == 2)
+  const uint16_t* bias;  // or NULL
+  uint16_t* out;
+  int64_t N, ldw0, ldw1, ldo;
+};
+struct GemvJob {
+  const uint16_t* x;
+  const uint16_t* resid;  // out = bf16(resid + bf16(result)), or NULL
+  int64_t M, K, ldx, ldr;
+  GemvSeg seg[kGemvMaxSegs];
   int64_t first[kGemvMaxSegs + 1];
   int count;
-  bool from_segs;  // the linears' operands come from here, not from GemmArgs
 };
 
 template <int NB, int ACT, bool BIAS, int MR>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g, GemvSegs sg) {
-  int seg = 0;  // launch-uniform per workgroup
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
+  int si = 0;  // launch-uniform per workgroup
 #pragma unroll
   for (int i = 1; i < kGemvMaxSegs; ++i)
-    if (i < sg.count && (int64_t)blockIdx.x >= sg.first[i]) seg = i;
-  if (sg.from_segs) {
-    g.w0 = g.w1 = sg.w[seg];
-    g.bias = sg.bias[seg];
-    g.out = sg.out[seg];
-    g.N = sg.N[seg];
-    g.ldw0 = g.ldw1 = sg.ldw[seg];
-    g.ldo = sg.ldo[seg];
-  }
+    if (i < job.count && (int64_t)blockIdx.x >= job.first[i]) si = i;
+  const GemvSeg& sg = job.seg[si];
+  const int64_t N = sg.N, K = job.K, M = job.M;
   constexpr int R = kGemvCols;
   constexpr int U = MR <= 2 ? 4 : 2;
   __shared__ float part[kGemvWaves][MR * NB * R];
   const int lane = (int)threadIdx.x & 63;
   const int wave = (int)threadIdx.x >> 6;
-  const int64_t n0 = ((int64_t)blockIdx.x - sg.first[seg]) * R;  // each segment covers its N
-  const int64_t chunks = g.K / 8;
+  const int64_t n0 = ((int64_t)blockIdx.x - job.first[si]) * R;  // each segment covers its N
+  const int64_t chunks = K / 8;
   // Columns past N (when N % R != 0) and x rows past M re-read the last
   // valid row; their results are not stored.
   const uint16_t* wr[NB][R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t n = n0 + r < g.N ? n0 + r : g.N - 1;
-    wr[0][r] = g.w0 + n * g.ldw0;
-    if constexpr (NB == 2) wr[NB - 1][r] = g.w1 + n * g.ldw1;
+    const int64_t n = n0 + r < N ? n0 + r : N - 1;
+    wr[0][r] = sg.w0 + n * sg.ldw0;
+    if constexpr (NB == 2) wr[NB - 1][r] = sg.w1 + n * sg.ldw1;
   }
   const uint16_t* xr[MR];
 #pragma unroll
-  for (int m = 0; m < MR; ++m) xr[m] = g.x + (m < g.M ? m : g.M - 1) * g.ldx;
+  for (int m = 0; m < MR; ++m) xr[m] = job.x + (m < M ? m : M - 1) * job.ldx;
   float acc[MR][NB][R];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
@@ -826,50 +825,56 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemmArgs g, GemvS
   // register indexing)
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    if (lane != m || m >= g.M) continue;
+    if (lane != m || m >= M) continue;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t n = n0 + r;
-      if (n >= g.N) continue;
-      const float bias = BIAS && g.bias ? bf2f(g.bias[n]) : 0.0f;
+      if (n >= N) continue;
+      const float bias = BIAS && sg.bias ? bf2f(sg.bias[n]) : 0.0f;
       float o = gemv_epilogue<NB, ACT, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
       // the eager residual add after the linear: two bf16 roundings
-      if (g.resid) o = rbf(o) + bf2f(g.resid[m * g.ldr + n]);
-      g.out[m * g.ldo + n] = (uint16_t)f2bf(o);
+      if (job.resid) o = rbf(o) + bf2f(job.resid[m * job.ldr + n]);
+      sg.out[m * sg.ldo + n] = (uint16_t)f2bf(o);
     }
   }
 }
 
 template <int NB, int ACT, bool BIAS>
-int launch_gemv_segs(const GemmArgs& g, const GemvSegs& sg, hipStream_t st) {
-  const int64_t grid = sg.first[sg.count];
+int launch_gemv_job(const GemvJob& job, hipStream_t st) {
+  const int64_t grid = job.first[job.count];
   if (grid <= 0 || grid > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   const dim3 gd((unsigned)grid), bd(kGemvWaves * 64);
-  if (g.M <= 1)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, g, sg);
-  else if (g.M <= 2)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, g, sg);
-  else if (g.M <= 4)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, g, sg);
+  if (job.M <= 1)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, job);
+  else if (job.M <= 2)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, job);
+  else if (job.M <= 4)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, job);
   else
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, g, sg);
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, job);
   return launch_status();
 }
 
-// One linear (or the P5 pair) as a single segment: one workgroup per
-// kGemvCols output columns.
-template <int NB, int ACT, bool BIAS>
-int launch_gemv(const GemmArgs& g, hipStream_t st) {
-  GemvSegs sg{};
-  sg.count = 1;
-  sg.first[0] = 0;
-  sg.first[1] = (g.N + kGemvCols - 1) / kGemvCols;
-  return launch_gemv_segs<NB, ACT, BIAS>(g, sg, st);
+// A one-segment job: one linear (or the P5 pair), one workgroup per
+// kGemvCols output columns; resid/ldr for the residual-add epilogue.
+GemvJob gemv_job(const GemmArgs& g, const uint16_t* resid = nullptr, int64_t ldr = 0) {
+  GemvJob job{};
+  job.x = g.x;
+  job.resid = resid;
+  job.M = g.M;
+  job.K = g.K;
+  job.ldx = g.ldx;
+  job.ldr = ldr;
+  job.seg[0] = GemvSeg{g.w0, g.w1, g.bias, g.out, g.N, g.ldw0, g.ldw1, g.ldo};
+  job.count = 1;
+  job.first[0] = 0;
+  job.first[1] = (g.N + kGemvCols - 1) / kGemvCols;
+  return job;
 }
 
 template <int NB, int ACT, bool BIAS>
 int launch_gemm(GemmArgs g, hipStream_t st) {
-  if (g.M <= kGemvMaxRows) return launch_gemv<NB, ACT, BIAS>(g, st);
+  if (g.M <= kGemvMaxRows) return launch_gemv_job<NB, ACT, BIAS>(gemv_job(g), st);
   const int64_t bn = NB == 1 ? kBW : kBW / 2;
   const int64_t tm = (g.M + kBM - 1) / kBM;
   const int64_t tn = (g.N + bn - 1) / bn;
@@ -1144,13 +1149,16 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
   if (M > kGemvMaxRows) return UMIC_ERR_UNSUPPORTED;
   if (!x || ldx < K) return UMIC_ERR_INVALID_ARG;
   if (K == 0) return UMIC_ERR_UNSUPPORTED;
-  GemvSegs sg{};
-  sg.count = count;
-  sg.from_segs = true;
+  GemvJob job{};
+  job.x = (const uint16_t*)x;
+  job.M = M;
+  job.K = K;
+  job.ldx = ldx;
+  job.count = count;
   bool any_bias = false;
   int64_t first = 0;
   for (int i = 0; i < count; ++i) {
-    sg.first[i] = first;
+    job.first[i] = first;
     if (N[i] == 0) continue;  // empty segment: no workgroups, pointers unused
     if (!w[i] || !out[i] || ldw[i] < K || ldo[i] < N[i]) return UMIC_ERR_INVALID_ARG;
     if (!gemm_shape_ok(x, w[i], w[i], out[i], M, N[i], K, ldx, ldw[i], ldw[i], ldo[i]))
@@ -1158,26 +1166,21 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
     const void* b = bias ? bias[i] : nullptr;
     if (b && ((uintptr_t)b & 7u)) return UMIC_ERR_UNSUPPORTED;
     any_bias = any_bias || b;
-    sg.w[i] = (const uint16_t*)w[i];
-    sg.bias[i] = (const uint16_t*)b;
-    sg.out[i] = (uint16_t*)out[i];
-    sg.N[i] = N[i];
-    sg.ldw[i] = ldw[i];
-    sg.ldo[i] = ldo[i];
+    job.seg[i] = GemvSeg{(const uint16_t*)w[i], (const uint16_t*)w[i], (const uint16_t*)b,
+                         (uint16_t*)out[i], N[i], ldw[i], ldw[i], ldo[i]};
     first += (N[i] + kGemvCols - 1) / kGemvCols;
   }
-  sg.first[count] = first;
+  job.first[count] = first;
   if (first == 0) return UMIC_OK;
-  GemmArgs g{(const uint16_t*)x, nullptr, nullptr, nullptr, nullptr, M, 0, K, ldx, 0, 0, 0, 0, 0};
   hipStream_t st = as_stream(stream);
   if (act == UMIC_ACT_GELU)
-    return any_bias ? launch_gemv_segs<1, UMIC_ACT_GELU, true>(g, sg, st)
-                    : launch_gemv_segs<1, UMIC_ACT_GELU, false>(g, sg, st);
+    return any_bias ? launch_gemv_job<1, UMIC_ACT_GELU, true>(job, st)
+                    : launch_gemv_job<1, UMIC_ACT_GELU, false>(job, st);
   if (act == UMIC_ACT_GELU_TANH)
-    return any_bias ? launch_gemv_segs<1, UMIC_ACT_GELU_TANH, true>(g, sg, st)
-                    : launch_gemv_segs<1, UMIC_ACT_GELU_TANH, false>(g, sg, st);
-  return any_bias ? launch_gemv_segs<1, UMIC_ACT_NONE, true>(g, sg, st)
-                  : launch_gemv_segs<1, UMIC_ACT_NONE, false>(g, sg, st);
+    return any_bias ? launch_gemv_job<1, UMIC_ACT_GELU_TANH, true>(job, st)
+                    : launch_gemv_job<1, UMIC_ACT_GELU_TANH, false>(job, st);
+  return any_bias ? launch_gemv_job<1, UMIC_ACT_NONE, true>(job, st)
+                  : launch_gemv_job<1, UMIC_ACT_NONE, false>(job, st);
 }
 
 extern "C" int umic_linear_add_bf16(const void* x, const void* w, const void* bias,
@@ -1193,8 +1196,9 @@ extern "C" int umic_linear_add_bf16(const void* x, const void* w, const void* bi
   if (!gemm_shape_ok(x, w, w, out, M, N, K, ldx, ldw, ldw, ldo)) return UMIC_ERR_UNSUPPORTED;
   if (bias && ((uintptr_t)bias & 7u)) return UMIC_ERR_UNSUPPORTED;
   GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
-             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0, (const uint16_t*)residual, ldr};
+             (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0};
+  const GemvJob job = gemv_job(g, (const uint16_t*)residual, ldr);
   hipStream_t st = as_stream(stream);
-  return bias ? launch_gemv<1, UMIC_ACT_NONE, true>(g, st)
-              : launch_gemv<1, UMIC_ACT_NONE, false>(g, st);
+  return bias ? launch_gemv_job<1, UMIC_ACT_NONE, true>(job, st)
+              : launch_gemv_job<1, UMIC_ACT_NONE, false>(job, st);
 }
