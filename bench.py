@@ -31,10 +31,11 @@ time.  ms_per_step is the sum over kernels of the per-launch event time.
 Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
 six fused norm/RoPE kernels (algorithmic bytes / summed durations);
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
-(by time) of the step; cpu_baseline = the CPU oracle (scalar C, one core)
-timed on a bounded sample of the same norm/RoPE workload, in GB/s;
-cpu_eager = the reference's own CPU path (HF's eager modules and RoPE
-functions in torch, all host threads) on the same sample.
+(by time) of the step; cpu_baseline = the reference's own CPU path (HF's
+eager Qwen3-VL modules, RoPE functions and the eager P5 chain in torch, bf16,
+on the host cores) over all five BASELINE configs at full size, value in GB/s
+over the norm/RoPE ops as for the GPU; cpu_oracle = the scalar C oracle (one
+core) on a bounded quarter-row sample of the norm/RoPE workload.
 layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
 prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
 HIP graph); --no-layer skips it.  kv_cache = text RoPE fused with the
@@ -119,13 +120,16 @@ def build_workload():
                                             _bf(1, M, 8, D, gen=g).transpose(1, 2)))
     rope_qkv = ring(8 * 16 * MV * 80, lambda: _bf(MV, 3, 16, 80, gen=g))
 
-    xg = _bf(M, H, gen=g)
-    wq = _bf(H, H, scale=0.02, gen=g)
-    wo = _bf(H, H, scale=0.02, gen=g)
-    wg = _bf(12288, H, scale=0.02, gen=g)
-    wu = _bf(12288, H, scale=0.02, gen=g)
-    wd = _bf(H, 12288, scale=0.02, gen=g)
-    hmid = _bf(M, 12288, gen=g)
+    # GEMM operand sets rotate like the norm inputs: a set (x, weights, and
+    # the output kept for one ring turn) comes back only after >= 640 MB
+    FF = 12288
+    proj = ring(2 * (2 * M * H + H * H), lambda: (_bf(M, H, gen=g), _bf(H, H, scale=0.02, gen=g),
+                                                   _bf(H, H, scale=0.02, gen=g)))
+    p5 = ring(2 * (M * H + 2 * FF * H + M * FF),
+              lambda: (_bf(M, H, gen=g), _bf(FF, H, scale=0.02, gen=g),
+                       _bf(FF, H, scale=0.02, gen=g)))
+    down = ring(2 * (M * FF + H * FF + M * H),
+                lambda: (_bf(M, FF, gen=g), _bf(H, FF, scale=0.02, gen=g)))
     qn_w, kn_w = _bf(D, scale=0.1, shift=1.0, gen=g), _bf(D, scale=0.1, shift=1.0, gen=g)
     eps = 1e-6
 
@@ -163,26 +167,31 @@ def build_workload():
         # the same work unfused: the two head-row norms, then the RoPE
         ("qk_norm_rope_unfused", lambda i: unfused_qk_norm_rope(*pick(rope_qk, i)),
          2 * b2 * (32 + 8) * M * D + 2 * b2 * M * D + 2 * b2 * D, 0, "hbm"),
-        ("q_proj", lambda i: linear.linear_hip(xg, wq), (M * H + H * H + M * H) * b2,
-         2 * M * H * H, "mfma"),
-        ("o_proj", lambda i: linear.linear_hip(xg, wo), (M * H + H * H + M * H) * b2,
-         2 * M * H * H, "mfma"),
-        ("gate_silu_mul", lambda i: fused_ffn.gate_silu_mul_hip(xg, wg.t(), wu.t()),
-         (M * H + 2 * 12288 * H + M * 12288) * b2, 2 * 2 * M * 12288 * H, "mfma"),
-        ("down_proj", lambda i: linear.linear_hip(hmid, wd),
-         (M * 12288 + H * 12288 + M * H) * b2, 2 * M * H * 12288, "mfma"),
-        ("down_proj_vendor", lambda i: torch.nn.functional.linear(hmid, wd),
-         (M * 12288 + H * 12288 + M * H) * b2, 2 * M * H * 12288, "mfma"),
+        ("q_proj", lambda i: linear.linear_hip(pick(proj, i)[0], pick(proj, i)[1]),
+         (M * H + H * H + M * H) * b2, 2 * M * H * H, "mfma"),
+        ("o_proj", lambda i: linear.linear_hip(pick(proj, i)[0], pick(proj, i)[2]),
+         (M * H + H * H + M * H) * b2, 2 * M * H * H, "mfma"),
+        ("gate_silu_mul", lambda i: fused_ffn.gate_silu_mul_hip(pick(p5, i)[0], pick(p5, i)[1].t(),
+                                                                pick(p5, i)[2].t()),
+         (M * H + 2 * FF * H + M * FF) * b2, 2 * 2 * M * FF * H, "mfma"),
+        ("down_proj", lambda i: linear.linear_hip(*pick(down, i)),
+         (M * FF + H * FF + M * H) * b2, 2 * M * H * FF, "mfma"),
+        ("down_proj_vendor", lambda i: torch.nn.functional.linear(*pick(down, i)),
+         (M * FF + H * FF + M * H) * b2, 2 * M * H * FF, "mfma"),
     ]
     rings = {"rmsnorm": len(rms_x), "add_rmsnorm": len(add_xr), "layernorm": len(ln_x),
              "add_layernorm": len(addln_xr), "rope_text": len(rope_qk),
-             "rope_vision": len(rope_qkv), "qk_norm_rope": len(rope_qk), "qk_norm_rope_unfused": len(rope_qk)}
-    spacer = lambda: fused_ffn.gate_silu_mul_hip(xg, wg.t(), wu.t())  # noqa: E731
+             "rope_vision": len(rope_qkv), "qk_norm_rope": len(rope_qk),
+             "qk_norm_rope_unfused": len(rope_qk), "q_proj": len(proj), "o_proj": len(proj),
+             "gate_silu_mul": len(p5), "down_proj": len(down), "down_proj_vendor": len(down)}
+    spacer = lambda: fused_ffn.gate_silu_mul_hip(p5[0][0], p5[0][1].t(), p5[0][2].t())  # noqa: E731
     return ents, rings, spacer
 
 
-def cpu_baseline(sample_s: float) -> dict:
-    """Time the CPU oracle on a bounded sample of the norm/RoPE workload."""
+def cpu_oracle(sample_s: float) -> dict:
+    """Time the CPU oracle (scalar C, one core) on a bounded sample of the
+    norm/RoPE workload: the restatement the parity tests check against,
+    reported beside the reference's own CPU path."""
     import numpy as np
 
     import oracle
@@ -230,60 +239,197 @@ def cpu_baseline(sample_s: float) -> dict:
                       f"{tot_t:.1f} s of single-thread scalar C"}
 
 
-def cpu_eager(sample_s: float) -> dict:
-    """The reference's own CPU path: its eager fallback, i.e. HF transformers'
-    Qwen3-VL RMSNorm module, nn.LayerNorm, the residual adds and HF's
-    apply_rotary_pos_emb / apply_rotary_pos_emb_vision, run by torch on the
-    host cores in bf16 (fp32 tables for vision, as HF builds them) on the same
-    quarter-row sample as cpu_baseline, bytes counted as for the GPU kernels."""
-    import torch
-    from transformers.models.qwen3_vl import modeling_qwen3_vl as hf
+def _host_cpu() -> dict:
+    """CPU model, the bf16 matrix/vector features torch's CPU kernels use,
+    and the cores this process may run on."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    feats = {k: k in flags for k in ("amx_bf16", "amx_tile", "avx512_bf16", "avx512f")}
+    return {"cpu_model": model, "cpu_flags": feats, "affinity_cpus": len(os.sched_getaffinity(0))}
 
+
+def cpu_reference(budget_s: float) -> dict:
+    """The reference's eager CPU path over the BASELINE configs, on the host.
+
+    The reference falls back to eager torch wherever a kernel is unavailable
+    (src/umic/kernels/fused_ffn.py:31-43 for P5; the modules' own forwards
+    for the norms, linears and RoPE), so its CPU path is HF transformers'
+    Qwen3-VL modules and functions run by torch in bf16:
+
+      config 1  RMSNorm [256,1024] -> HF MLP 1024->3072->1024 (silu)
+      config 2  RMSNorm, residual add + RMSNorm [3100,4096];
+                LayerNorm, residual add + LayerNorm [16384,1280]
+      config 3  gate_silu_mul_eager [3100,4096] x [4096,12288] x 2, down_proj
+                F.linear 12288->4096, q_proj / o_proj F.linear 4096->4096
+      config 4  apply_rotary_pos_emb q [1,32,3100,128] k [1,8,3100,128];
+                apply_rotary_pos_emb_vision q, k [16384,16,80], fp32 tables
+      config 5  one Qwen3-VL text decoder layer, prefill M=3100, then one
+                decode step (M=1) on the prefill's KV cache
+
+    Full BASELINE sizes.  Inputs are drawn in fp32 with a fixed seed and cast
+    to bf16.  Each op: 2 warm-up calls, then the median of 5 (1 and 3 for the
+    M=3100 GEMMs and the layer); an op whose first call shows the budget
+    would be exceeded gets fewer repetitions (at least one timed call).
+    Threads: every CPU of this process's affinity mask, capped by
+    OMP_NUM_THREADS when the environment sets it (the host share of a
+    one-GPU box).  value = the norm/RoPE ops' bytes (counted as for the GPU
+    kernels) over their summed medians, in GB/s, as the GPU's value."""
+    import torch
+    from torch.nn import functional as F
+    from transformers.models.qwen3_vl import modeling_qwen3_vl as hf
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLTextConfig
+
+    host = _host_cpu()
+    threads = host["affinity_cpus"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, max(1, int(os.environ["OMP_NUM_THREADS"])))
+    torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
 
     def bfr(*shape, scale=1.0, shift=0.0):
-        return (shift + scale * torch.randn(*shape, generator=gen)).to(torch.bfloat16)
+        return (shift + scale * torch.randn(*shape, generator=gen)).to(bf)
 
-    M, H, MV, HV, D = 3100 // 4, 4096, 16384 // 4, 1280, 128
-    x, r = bfr(M, H), bfr(M, H)
-    rms = hf.Qwen3VLTextRMSNorm(H, eps=1e-6)
-    xv, rv = bfr(MV, HV), bfr(MV, HV)
-    ln = torch.nn.LayerNorm(HV, eps=1e-6)
-    with torch.no_grad():
-        rms.weight.copy_(bfr(H, scale=0.1, shift=1.0).float())
-        ln.weight.copy_(bfr(HV, scale=0.1, shift=1.0).float())
-        ln.bias.copy_(bfr(HV, scale=0.1).float())
-    rms, ln = rms.to(torch.bfloat16), ln.to(torch.bfloat16)
-    q, k = bfr(1, M, 32, D).transpose(1, 2), bfr(1, M, 8, D).transpose(1, 2)
-    ct, st = bfr(1, M, D), bfr(1, M, D)
-    vq, vk = bfr(MV, 16, 80), bfr(MV, 16, 80)
-    cv, sv = torch.randn(MV, 80, generator=gen), torch.randn(MV, 80, generator=gen)
-    work = [
-        (lambda: rms(x), 4 * M * H),
-        (lambda: rms(x + r), 8 * M * H),
-        (lambda: ln(xv), 4 * MV * HV),
-        (lambda: ln(xv + rv), 8 * MV * HV),
-        (lambda: hf.apply_rotary_pos_emb(q, k, ct, st), 4 * 40 * M * D + 4 * M * D),
-        (lambda: hf.apply_rotary_pos_emb_vision(vq, vk, cv, sv), 4 * 32 * MV * 80 + 8 * MV * 80),
-    ]
-    tot_b, tot_t, passes = 0, 0.0, 0
-    with torch.no_grad():
-        for fn, _ in work:   # first-call setup out of the timing
+    t_budget = time.perf_counter() + budget_s
+    ms: dict[str, float] = {}
+    reps_used: dict[str, int] = {}
+
+    def timed(name, fn, warm=2, reps=5):
+        t0 = time.perf_counter()
+        fn()
+        first = time.perf_counter() - t0  # the first warm-up call
+        fit = int((t_budget - time.perf_counter()) / max(first, 1e-6))  # calls that fit
+        reps = max(1, min(reps, fit))
+        warm = max(0, min(warm - 1, fit - reps))
+        for _ in range(warm):
             fn()
-        t_end = time.perf_counter() + sample_s
-        while time.perf_counter() < t_end or passes == 0:
-            for fn, nbytes in work:
-                t0 = time.perf_counter()
-                fn()
-                tot_t += time.perf_counter() - t0
-                tot_b += nbytes
-            passes += 1
-    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s",
-            "cores": torch.get_num_threads(), "kind": "reference eager (torch CPU)",
-            "sample": f"{passes} pass(es) of HF's eager RMSNorm, add+RMSNorm, LayerNorm, "
-                      f"add+LayerNorm, text and vision RoPE on 1/4 of the BASELINE rows "
-                      f"({tot_b / passes / 1e6:.0f} MB per pass), {tot_t:.1f} s, bf16 on "
-                      f"{torch.get_num_threads()} threads"}
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        ms[name] = round(ts[len(ts) // 2] * 1e3, 3)
+        reps_used[name] = reps
+
+    def text_cfg(hidden, inter, heads=32, kv=8, hd=128):
+        return Qwen3VLTextConfig(hidden_size=hidden, intermediate_size=inter,
+                                 num_attention_heads=heads, num_key_value_heads=kv,
+                                 head_dim=hd, num_hidden_layers=1, rms_norm_eps=1e-6,
+                                 hidden_act="silu",
+                                 rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+                                 attn_implementation="sdpa")
+
+    def init_(mod):
+        with torch.no_grad():
+            for n, p in mod.named_parameters():
+                if "norm" in n:
+                    p.copy_(1 + 0.1 * torch.randn(p.shape, generator=gen))
+                else:
+                    p.copy_(0.02 * torch.randn(p.shape, generator=gen))
+        return mod.to(bf).eval()
+
+    M, H, MV, HV, D = 3100, 4096, 16384, 1280, 128
+    nbytes = {}
+    with torch.no_grad():
+        # config 1: the CPU-eager MLP block
+        c1 = text_cfg(1024, 3072, heads=8, kv=8, hd=128)
+        norm1, mlp1 = init_(hf.Qwen3VLTextRMSNorm(1024, eps=1e-6)), init_(hf.Qwen3VLTextMLP(c1))
+        x1 = bfr(256, 1024)
+        timed("c1_mlp_block", lambda: mlp1(norm1(x1)))
+
+        # config 2: the norms at full size
+        x, r = bfr(M, H), bfr(M, H)
+        rms = init_(hf.Qwen3VLTextRMSNorm(H, eps=1e-6))
+        xv, rv = bfr(MV, HV), bfr(MV, HV)
+        ln = torch.nn.LayerNorm(HV, eps=1e-6)
+        with torch.no_grad():
+            ln.weight.copy_(bfr(HV, scale=0.1, shift=1.0).float())
+            ln.bias.copy_(bfr(HV, scale=0.1).float())
+        ln = ln.to(bf)
+        timed("rmsnorm", lambda: rms(x))
+        timed("add_rmsnorm", lambda: rms(x + r))
+        timed("layernorm", lambda: ln(xv))
+        timed("add_layernorm", lambda: ln(xv + rv))
+        nbytes.update(rmsnorm=4 * M * H + 2 * H, add_rmsnorm=8 * M * H + 2 * H,
+                      layernorm=4 * MV * HV + 4 * HV, add_layernorm=8 * MV * HV + 4 * HV)
+        del x, r, xv, rv
+
+        # config 4: RoPE at full size (q/k as transposed projection views)
+        q, k = bfr(1, M, 32, D).transpose(1, 2), bfr(1, M, 8, D).transpose(1, 2)
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        emb = torch.arange(M, dtype=torch.float32)[:, None] * inv[None]
+        emb = torch.cat((emb, emb), -1)
+        ct, st = emb.cos().to(bf)[None], emb.sin().to(bf)[None]
+        vq, vk = bfr(MV, 16, 80), bfr(MV, 16, 80)
+        cv, sv = torch.randn(MV, 80, generator=gen), torch.randn(MV, 80, generator=gen)
+        timed("rope_text", lambda: hf.apply_rotary_pos_emb(q, k, ct, st))
+        timed("rope_vision", lambda: hf.apply_rotary_pos_emb_vision(vq, vk, cv, sv))
+        nbytes.update(rope_text=4 * 40 * M * D + 4 * M * D,
+                      rope_vision=4 * 32 * MV * 80 + 8 * MV * 80)
+        del q, k, vq, vk
+
+        # config 3: the M=3100 projections, W ~ N(0, 0.02)
+        xg = bfr(M, H)
+        wg, wu = bfr(12288, H, scale=0.02), bfr(12288, H, scale=0.02)
+        wd, wq, wo = bfr(H, 12288, scale=0.02), bfr(H, H, scale=0.02), bfr(H, H, scale=0.02)
+        ffn_eager = lambda a, g_, u_: F.silu(a @ g_) * (a @ u_)  # noqa: E731  fused_ffn.py:43
+        hmid = ffn_eager(xg, wg.t(), wu.t())
+        timed("gate_silu_mul", lambda: ffn_eager(xg, wg.t(), wu.t()), warm=1, reps=3)
+        timed("down_proj", lambda: F.linear(hmid, wd), warm=1, reps=3)
+        timed("q_proj", lambda: F.linear(xg, wq), warm=1, reps=3)
+        timed("o_proj", lambda: F.linear(xg, wo), warm=1, reps=3)
+        del xg, wg, wu, wd, wq, wo, hmid
+
+        # config 5: one decoder layer, prefill then one decode step
+        c5 = text_cfg(H, 12288)
+        layer = init_(hf.Qwen3VLTextDecoderLayer(c5, 0))
+        rot = hf.Qwen3VLTextRotaryEmbedding(c5)
+        h0 = bfr(1, M, H)
+        pos = torch.arange(M)[None]
+        cs = rot(h0, pos)
+        from transformers.cache_utils import DynamicCache
+
+        def prefill():
+            cache = DynamicCache()
+            layer(h0, position_embeddings=cs, past_key_values=cache, position_ids=pos)
+            return cache
+
+        timed("layer_prefill", prefill, warm=1, reps=3)
+        cache = prefill()
+        h1 = bfr(1, 1, H)
+        cs1 = rot(h1, torch.tensor([[M]]))
+
+        def decode():
+            layer(h1, position_embeddings=cs1, past_key_values=cache,
+                  position_ids=torch.tensor([[M]]))
+            cache.crop(-1)
+
+        timed("layer_decode", decode)
+
+    sites = list(nbytes)
+    tot_ms = sum(ms[n] for n in sites)
+    value = sum(nbytes.values()) / (tot_ms * 1e-3) / 1e9
+    flops = {"gate_silu_mul": 4 * M * 12288 * H, "down_proj": 2 * M * H * 12288,
+             "q_proj": 2 * M * H * H, "o_proj": 2 * M * H * H}
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "mlp_prefill_ms": round(ms["gate_silu_mul"] + ms["down_proj"], 3),
+            "ms": ms, "reps": reps_used,
+            "gemm_tflops": {n: round(f / (ms[n] * 1e-3) / 1e12, 3) for n, f in flops.items()},
+            **host,
+            "sample": "the reference's eager CPU path (HF transformers Qwen3-VL modules and "
+                      "RoPE functions, fused_ffn.py:31-43's gate_silu_mul_eager, F.linear) "
+                      "on all five BASELINE configs at full size, bf16, torch on "
+                      f"{threads} threads; value over the six norm/RoPE ops "
+                      f"({sum(nbytes.values()) / 1e6:.0f} MB in {tot_ms:.1f} ms)"}
 
 
 def load_traffic(name: str):
@@ -614,8 +760,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-sample-s", type=float, default=12.0)
+    ap.add_argument("--cpu-sample-s", type=float, default=6.0,
+                    help="seconds of scalar-oracle timing (cpu_oracle)")
+    ap.add_argument("--cpu-budget-s", type=float, default=45.0,
+                    help="seconds the reference's eager CPU path may take (cpu_baseline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-only", action="store_true",
+                    help="print only the CPU baselines (no GPU needed)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
     ap.add_argument("--copy-ceiling", action="store_true",
@@ -636,6 +787,10 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.cpu_only:
+        print(json.dumps({"cpu_baseline": cpu_reference(args.cpu_budget_s),
+                          "cpu_oracle": cpu_oracle(args.cpu_sample_s)}), flush=True)
+        return 0
     if args.pmc_probe:
         return pmc_probe()
     if args.copy_ceiling:
@@ -729,8 +884,8 @@ def main() -> int:
         "roofline": roof,
         "layer": None if args.no_layer else layer_step(),
         "kv_cache": None if args.no_kv_cache else kv_cache_step(),
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_s),
-        "cpu_eager": None if args.no_cpu_baseline else cpu_eager(args.cpu_sample_s / 2),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_reference(args.cpu_budget_s),
+        "cpu_oracle": None if args.no_cpu_baseline else cpu_oracle(args.cpu_sample_s),
     }
     print(json.dumps(out), flush=True)
     return 0
