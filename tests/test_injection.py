@@ -420,6 +420,16 @@ def test_find_lm_module_variants():
     root.vlm.language_model = outer
     assert optimize.find_lm_module(root) is outer
     assert optimize.find_lm_module(nn.Linear(2, 2)) is None
+    # transformers >= 5: vlm.model is the VLM trunk holding language_model / visual
+    vis = tiny_vision_model()
+    trunk = nn.Module()
+    trunk.language_model, trunk.visual = lm, vis
+    root5 = nn.Module()
+    root5.vlm = nn.Module()
+    root5.vlm.model = trunk
+    assert optimize.find_lm_module(root5) is lm
+    assert optimize.find_visual_module(root5) is vis
+    assert optimize.find_visual_module(_wrap(visual=vis)) is vis
 
 
 def test_decode_paths_defer_to_hooked_modules():
