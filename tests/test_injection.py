@@ -460,3 +460,23 @@ def test_decode_paths_defer_to_hooked_modules():
     h.remove()
     integrate.unfuse_mlps(lm)
     assert seen == [attn.k_proj]
+
+
+def test_kernel_registry():
+    """The reference's registry surface (src/umic/kernels/__init__.py:14-23),
+    pre-populated with the HIP wrappers; a registration replaces an entry."""
+    from umic import kernels
+    from umic.kernels import layernorm, rmsnorm, rope
+
+    assert kernels.get_kernel("rmsnorm") is rmsnorm.rmsnorm_hip
+    assert kernels.get_kernel("add_layernorm") is layernorm.add_layernorm_hip
+    assert kernels.get_kernel("rope_vision") is rope.apply_rotary_vision_hip
+    assert kernels.get_kernel("gate_silu_mul") is fused_ffn.gate_silu_mul_hip
+    assert kernels.get_kernel("linear") is linear.linear_hip
+    assert kernels.get_kernel("no_such_pattern") is None
+    mine = lambda *a: None  # noqa: E731
+    kernels.register_kernel("rmsnorm", mine)
+    try:
+        assert kernels.get_kernel("rmsnorm") is mine
+    finally:
+        kernels.register_kernel("rmsnorm", rmsnorm.rmsnorm_hip)
