@@ -70,7 +70,7 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
     # q_proj, o_proj and, at prefill (stream-K shape), the MLP's down_proj,
     # all through the workspace entry point; at decode the down projection
     # carries the MLP residual add in its epilogue
-    down_add = 1 if M <= integrate.GEMV_MAX_ROWS else 0
+    down_add = 1 if M <= integrate.GEMV_ROWS_DOWN else 0
     assert call_log["umic_linear_add_bf16"] == down_add
     assert (call_log["umic_linear_ws_bf16"] + call_log["umic_linear_bf16"]
             == 3 * gemm_calls - down_add)

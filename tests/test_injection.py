@@ -169,8 +169,9 @@ def test_cpu_patched_vision_model_is_bit_identical():
 
 def test_fuse_min_rows_boundary(monkeypatch):
     """63 rows run the eager class forward; 64 rows take the fused kernel;
-    decode-sized calls (up to GEMV_MAX_ROWS rows) take the library's GEMV,
-    the MLP's down projection included, and one row more is eager again."""
+    decode-sized calls take the library's GEMV up to each site's measured
+    limit (P5 and q/o_proj 4 rows, the MLP's down projection 2), and the
+    rows above it the vendor path again."""
     calls = []
 
     def fake_p5(x, wg_kn, wu_kn):
@@ -189,13 +190,16 @@ def test_fuse_min_rows_boundary(monkeypatch):
     integrate.fuse_mlps(m)
     integrate.fuse_linears(m)
     mlp, q = m.layers[0].mlp, m.layers[0].self_attn.q_proj
-    for rows in (8, 9, 63, 64):
+    for rows in (2, 3, 4, 5, 8, 63, 64):
         x = torch.randn(1, rows, 128).to(BF)
         with torch.no_grad():
             mlp(x)
             q(x)
-    assert calls == [("p5", 8), ("lin", 8), ("lin", 8), ("p5", 64), ("lin", 64)]
+    assert calls == [("p5", 2), ("lin", 2), ("lin", 2), ("p5", 3), ("lin", 3), ("p5", 4),
+                     ("lin", 4), ("p5", 64), ("lin", 64)]
     assert integrate.FUSE_MIN_ROWS == 64 and integrate.GEMV_MAX_ROWS == 8
+    assert (integrate.GEMV_ROWS_MLP, integrate.GEMV_ROWS_LINEAR,
+            integrate.GEMV_ROWS_DOWN) == (4, 4, 2)
 
 
 def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):

@@ -733,7 +733,11 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
   const GemvSeg& sg = job.seg[si];
   const int64_t N = sg.N, K = job.K, M = job.M;
   constexpr int R = kGemvCols;
-  constexpr int U = MR <= 2 ? 4 : 2;
+  // Slabs in flight per lane.  With U = 4 a workgroup's waves cover 1024
+  // chunks per pass, but K = 4096 has 512: half the waves sat idle, and the
+  // config-5 decode sites ran 11-22% slower than with U = 2 (graph-timed on
+  // MI355X).  Eight rows hold eight x slabs per weight slab: U = 1 there.
+  constexpr int U = MR >= 8 ? 1 : 2;
   __shared__ float part[kGemvWaves][MR * NB * R];
   const int lane = (int)threadIdx.x & 63;
   const int wave = (int)threadIdx.x >> 6;

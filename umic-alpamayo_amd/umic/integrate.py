@@ -12,7 +12,7 @@ hooks, and deleting the attribute restores the class forward.
 Each replacement forward first decides whether the fused gfx950 kernel
 reproduces the module on the given inputs (GPU bf16 tensors of a handled
 layout; for the GEMM sites also at least FUSE_MIN_ROWS rows, or at most
-GEMV_MAX_ROWS (the decode GEMV); and no
+the site's GEMV row limit (the decode GEMV); and no
 gradient to carry, since the kernels have no backward).  If not, it runs
 the module's own class forward -- the original eager math on whatever
 device the inputs live on, recorded by autograd as usual.  If the inputs are eligible but libumic_hip.so
@@ -41,18 +41,27 @@ _SILU_NAMES = ("silu", "swish")
 # one fused launch always replaces several eager ones.
 FUSE_MIN_ROWS = 64
 
-# ...except for the fewest rows, the decode steps: with 1..GEMV_MAX_ROWS
-# rows the library's entry points run a weight-streaming GEMV kernel that
-# measured 2-4x hipBLASLt's GEMVs on the config-5 decode shapes, so the text
-# MLP and projections take it there (P5 with its silu(g) * u epilogue, the
-# down projection, q/k/v/o).  Between the two bounds the vendor path stays.
-GEMV_MAX_ROWS = 8
+# ...except for the fewest rows, the decode steps: there the library's entry
+# points run a weight-streaming GEMV kernel (up to GEMV_MAX_ROWS rows).  Per
+# site, the rows where it beat hipBLASLt on the config-5 decode shapes (one
+# MI355X, every launch in a HIP graph over rotating weights, GEMV time as a
+# fraction of the vendor's):
+#   q/k/v in one launch (N = 4096 + 1024 + 1024, K = 4096): 1-8 rows, 0.24-0.62
+#   q_proj / o_proj (N = 4096, K = 4096): 1-4 rows, 0.52-0.77 (5 rows: 1.15)
+#   P5 gate/up (N = 2 x 12288, K = 4096): 1-4 rows, 0.54-0.67 (5 rows: 1.16)
+#   down_proj (N = 4096, K = 12288): 1-2 rows, 0.89-0.98 (3 rows: 1.22)
+# Rows between a site's limit and FUSE_MIN_ROWS stay on the vendor path.
+GEMV_MAX_ROWS = 8     # the library's GEMV limit; the q/k/v launch takes it all
+GEMV_ROWS_LINEAR = 4  # q_proj / o_proj
+GEMV_ROWS_MLP = 4     # the P5 gate/up GEMV
+GEMV_ROWS_DOWN = 2    # the MLP's down projection (and its residual epilogue)
 
 
-def _gemm_rows_ok(x: torch.Tensor) -> bool:
-    """Row count in one of the fused GEMM regimes (GEMV or tiled)."""
+def _gemm_rows_ok(x: torch.Tensor, gemv_rows: int) -> bool:
+    """Row count in one of a site's fused GEMM regimes: tiled from
+    FUSE_MIN_ROWS, GEMV up to gemv_rows."""
     rows = _rows(x)
-    return rows >= FUSE_MIN_ROWS or 1 <= rows <= GEMV_MAX_ROWS
+    return rows >= FUSE_MIN_ROWS or 1 <= rows <= gemv_rows
 
 
 def _hooked(*mods) -> bool:
@@ -66,9 +75,9 @@ def _hooked(*mods) -> bool:
     return any(m is not None and (m._forward_hooks or m._forward_pre_hooks) for m in mods)
 
 
-def _linear(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """mod(x) for an nn.Linear, on the library's GEMV in the decode regime."""
-    if (isinstance(mod, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS and not _hooked(mod)
+def _linear(mod: nn.Module, x: torch.Tensor, gemv_rows: int = GEMV_ROWS_LINEAR) -> torch.Tensor:
+    """mod(x) for an nn.Linear, on the library's GEMV for 1..gemv_rows rows."""
+    if (isinstance(mod, nn.Linear) and 1 <= _rows(x) <= gemv_rows and not _hooked(mod)
             and linear.linear_eligible(x, mod.weight, mod.bias)
             and not grad_needed(x, mod.weight, mod.bias)):
         return linear.linear_hip(x, mod.weight, mod.bias)
@@ -124,15 +133,15 @@ def _is_p5_mlp(module: nn.Module) -> bool:
 def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """P5-fused replacement: silu(x@Wg)*(x@Wu) in one kernel, then down."""
     wg, wu = self.gate_proj.weight, self.up_proj.weight
-    if (not _gemm_rows_ok(x) or not fused_ffn.p5_eligible(x, wg, wu)
+    if (not _gemm_rows_ok(x, GEMV_ROWS_MLP) or not fused_ffn.p5_eligible(x, wg, wu)
             or grad_needed(x, wg, wu)):
         return _eager(self, x)
     # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
     # takes -- the kernel reads the original weight memory.
     h = fused_ffn.gate_silu_mul_hip(x, wg.t(), wu.t())
     down = self.down_proj
-    if _rows(h) <= GEMV_MAX_ROWS:
-        return _linear(down, h)
+    if _rows(h) < FUSE_MIN_ROWS:
+        return _linear(down, h, GEMV_ROWS_DOWN)
     if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear)
             and linear.linear_eligible(h, down.weight, down.bias)
             and linear.stream_k_planned(h, down.weight)):
@@ -164,7 +173,8 @@ def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
 def _patched_linear_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
     """Route large-M and decode calls to the fused linear (tiled or GEMV);
     the rows between stay on the vendor BLAS."""
-    if (not _gemm_rows_ok(x) or not linear.linear_eligible(x, self.weight, self.bias)
+    if (not _gemm_rows_ok(x, GEMV_ROWS_LINEAR)
+            or not linear.linear_eligible(x, self.weight, self.bias)
             or grad_needed(x, self.weight, self.bias)):
         return _eager(self, x)
     return linear.linear_hip(x, self.weight, self.bias)
@@ -267,7 +277,7 @@ def _fused_residual_layer_forward(self, hidden_states, position_embeddings=None,
 
 
 def _decode_mlp_residual(mlp: nn.Module, x: torch.Tensor, residual: torch.Tensor):
-    """residual + mlp(x) for a P5-fused MLP at decode (1..GEMV_MAX_ROWS rows):
+    """residual + mlp(x) for a P5-fused MLP at decode (1..GEMV_ROWS_DOWN rows):
     the fused gate_silu_mul GEMV, then down_proj with the residual add in
     its epilogue (umic_linear_add_bf16, the eager chain's two roundings).
     None when the MLP is not the fused one or the call is not eligible."""
@@ -277,7 +287,7 @@ def _decode_mlp_residual(mlp: nn.Module, x: torch.Tensor, residual: torch.Tensor
     if _hooked(mlp, down):
         return None
     wg, wu = mlp.gate_proj.weight, mlp.up_proj.weight
-    if not (isinstance(down, nn.Linear) and 1 <= _rows(x) <= GEMV_MAX_ROWS
+    if not (isinstance(down, nn.Linear) and 1 <= _rows(x) <= GEMV_ROWS_DOWN
             and fused_ffn.p5_eligible(x, wg, wu)
             and residual.dtype == x.dtype and residual.device == x.device
             and residual.shape == (*x.shape[:-1], down.weight.shape[0])
