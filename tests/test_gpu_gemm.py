@@ -141,6 +141,7 @@ def test_stream_k_deterministic_and_close_to_data_parallel():
 
     M, N, K = 3100, 4096, 12288
     assert _sk_bytes(M, N, K) > 0
+    print(f"stream-K M={M} N={N} K={K}", flush=True)
     torch.manual_seed(5)
     x = torch.randn(M, K).to(torch.bfloat16).to(DEV)
     w = (torch.randn(N, K) * 0.02).to(torch.bfloat16).to(DEV)
@@ -156,6 +157,30 @@ def test_stream_k_deterministic_and_close_to_data_parallel():
     # larger ulp counts only where the output is near zero (cancellation):
     # no difference exceeds one bf16 ulp of the largest output (2^-7 relative)
     assert ((y1.float() - ydp.float()).abs().max() / ydp.float().abs().max()).item() <= 2.0 ** -7
+
+
+def test_stream_k_workspace_shared_across_shapes():
+    """One stream's workspace serves stream-K calls of any shape in turn: the
+    tile counters sit in a fixed region ahead of every call's partial slots,
+    so a call with few tiles never stores partials where a later call with
+    more tiles counts arrivals.  Shapes of 4, 208, 8, 96, 32 and 208 tiles,
+    in turn, each against the data-parallel kernel."""
+    from umic import _lib
+
+    g = torch.Generator().manual_seed(13)
+    for M, N, K in [(300, 264, 12288), (3100, 4096, 12288), (32, 2048, 12288),
+                    (1536, 4096, 12288), (300, 4096, 12288), (3100, 4096, 12288)]:
+        print(f"shared workspace: M={M} N={N} K={K}", flush=True)
+        assert _sk_bytes(M, N, K) > 0
+        x = bf16_randn(M, K, gen=g).to(DEV)
+        w = bf16_randn(N, K, scale=0.02, gen=g).to(DEV)
+        y = linear.linear_hip(x, w)
+        ydp = torch.empty_like(y)
+        _lib.call("umic_linear_bf16", x.data_ptr(), w.data_ptr(), None, ydp.data_ptr(), M, N, K,
+                  K, K, N, 0, _lib.stream_of(x))
+        torch.cuda.synchronize()
+        err = ((y.float() - ydp.float()).abs().max() / ydp.float().abs().max()).item()
+        assert err <= 2.0 ** -7, (M, N, K, err)
 
 
 def test_down_proj_full_shape_vs_fp32():

@@ -496,6 +496,13 @@ struct SkArgs {
 };
 constexpr int kSlotVec = kBM * kBW / 4;  // f32x4 per partial tile (256 KB)
 constexpr int kSkMaxSeg = 3;             // segments per tile (checked on the host)
+// Workspace layout: the tile counters in a region of fixed size, then the
+// partial slots.  One workspace serves calls of any shape in turn, so no
+// call's slots may overlap another call's counters: with the counter region
+// sized by the call's own tile count, a call with few tiles stored partials
+// where a later call with more tiles kept (and trusted) zero counters.
+constexpr int kSkMaxTiles = 1024;        // stream-K needs fewer tiles than CUs
+constexpr int64_t kSkCounterBytes = 2 * kSkMaxTiles * (int64_t)sizeof(int);
 
 // Tail units: v = t * L + r is step ks + r of tile t (L = KT - ks); tail
 // workgroup j owns [j*Ut/Gt, (j+1)*Ut/Gt), Ut = T*L, Gt = G - T (Ut*Gt < 2^31,
@@ -931,6 +938,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   const int64_t KT = K / kBK;
   const int64_t G = std::min<int64_t>(cus, 2 * T - 1);
   if (cus <= 0 || G <= T || T * KT * G >= ((int64_t)1 << 31)) return pl;
+  if (T > kSkMaxTiles) return pl;
   // Main workgroups take a sixth of the tail beyond the even share, which
   // offsets the tail workgroups' extra segment prologues and partial stores
   // and makes a main workgroup usually the last to arrive at its tile.
@@ -944,7 +952,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   pl.G = (int)G;
   pl.KT = (int)KT;
   pl.ks = (int)ks;
-  pl.counter_bytes = (2 * T * (int64_t)sizeof(int) + 255) / 256 * 256;
+  pl.counter_bytes = kSkCounterBytes;
   pl.bytes = pl.counter_bytes + T * kSkMaxSeg * kSlotVec * (int64_t)sizeof(f32x4_t);
   return pl;
 }
