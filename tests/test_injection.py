@@ -168,10 +168,10 @@ def test_cpu_patched_vision_model_is_bit_identical():
 # ---- FUSE_MIN_ROWS regime dispatch ----------------------------------------
 
 def test_fuse_min_rows_boundary(monkeypatch):
-    """63 rows run the eager class forward; 64 rows take the fused kernel;
-    decode-sized calls take the library's GEMV up to each site's measured
-    limit (P5 and q/o_proj 4 rows, the MLP's down projection 2), and the
-    rows above it the vendor path again."""
+    """Decode-sized calls take the library's GEMV up to each site's measured
+    limit (P5 and q/o_proj 4 rows, the MLP's down projection 2); from there
+    the vendor path, until a site's tiled kernel wins: P5 from 256 rows, the
+    plain q/o linear never."""
     calls = []
 
     def fake_p5(x, wg_kn, wu_kn):
@@ -190,21 +190,30 @@ def test_fuse_min_rows_boundary(monkeypatch):
     integrate.fuse_mlps(m)
     integrate.fuse_linears(m)
     mlp, q = m.layers[0].mlp, m.layers[0].self_attn.q_proj
-    for rows in (2, 3, 4, 5, 8, 63, 64):
+    for rows in (2, 3, 4, 5, 8, 63, 64, 255, 256):
         x = torch.randn(1, rows, 128).to(BF)
         with torch.no_grad():
             mlp(x)
             q(x)
     assert calls == [("p5", 2), ("lin", 2), ("lin", 2), ("p5", 3), ("lin", 3), ("p5", 4),
-                     ("lin", 4), ("p5", 64), ("lin", 64)]
+                     ("lin", 4), ("p5", 256)]
     assert integrate.FUSE_MIN_ROWS == 64 and integrate.GEMV_MAX_ROWS == 8
     assert (integrate.GEMV_ROWS_MLP, integrate.GEMV_ROWS_LINEAR,
             integrate.GEMV_ROWS_DOWN) == (4, 4, 2)
+    assert (integrate.TILED_MIN_ROWS_MLP, integrate.TILED_MIN_ROWS_LINEAR) == (256, None)
+    # a site's tiled kernel can be re-enabled from a chosen row count
+    monkeypatch.setattr(integrate, "TILED_MIN_ROWS_LINEAR", 64)
+    calls.clear()
+    with torch.no_grad():
+        q(torch.randn(1, 64, 128).to(BF))
+        q(torch.randn(1, 63, 128).to(BF))
+    assert calls == [("lin", 64)]
 
 
 def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):
-    """The ViT MLP's fc1 takes the fused linear from 64 rows, with the GELU
-    form the module computes (Qwen3-VL's ViT: gelu_pytorch_tanh)."""
+    """The ViT MLP's fc1 takes the fused linear from TILED_MIN_ROWS_GELU_MLP
+    (2048) rows, where it stops losing to the vendor path, with the GELU form
+    the module computes (Qwen3-VL's ViT: gelu_pytorch_tanh)."""
     calls = []
 
     def fake_lin(x, w, b=None, act=None):
@@ -217,10 +226,10 @@ def test_gelu_mlp_min_rows_and_activation_kind(monkeypatch):
     m = tiny_vision_model()
     integrate.fuse_gelu_mlps(m)
     mlp = m.blocks[0].mlp
-    for rows in (63, 64):
+    for rows in (64, 2047, 2048):
         with torch.no_grad():
             mlp(torch.randn(rows, 64).to(BF))
-    assert calls == [(64, "gelu_tanh")]
+    assert calls == [(2048, "gelu_tanh")]
 
 
 def test_autograd_keeps_the_eager_path(monkeypatch):
@@ -254,7 +263,7 @@ def test_autograd_keeps_the_eager_path(monkeypatch):
     integrate.fuse_linears(m)
     integrate.fuse_rmsnorms(m)
     mlp, q, norm = m.layers[0].mlp, m.layers[0].self_attn.q_proj, m.norm
-    x = torch.randn(1, 64, 128).to(BF)
+    x = torch.randn(1, 4, 128).to(BF)  # the GEMV regime of P5 and q_proj
     assert mlp.gate_proj.weight.requires_grad
     out = mlp(x)
     q(x)

@@ -57,11 +57,38 @@ GEMV_ROWS_MLP = 4     # the P5 gate/up GEMV
 GEMV_ROWS_DOWN = 2    # the MLP's down projection (and its residual epilogue)
 
 
-def _gemm_rows_ok(x: torch.Tensor, gemv_rows: int) -> bool:
-    """Row count in one of a site's fused GEMM regimes: tiled from
-    FUSE_MIN_ROWS, GEMV up to gemv_rows."""
+# The tiled MFMA kernels against the vendor path they replace, per site and
+# row count (config-5 and ViT shapes, one MI355X, every launch in a HIP graph
+# over rotating operands; fused time / vendor time):
+#   P5 gate/up + SiLU*mul (K = 4096, N = 2 x 12288) vs two GEMMs, silu, mul:
+#     M = 64: 1.48, 256: 0.93, 512: 0.85, 1024: 1.02, 2048: 0.89, 3100: 0.90, 4096: 0.99
+#   ViT fc1 + bias + tanh GELU (K = 1280, N = 5120) vs F.linear then F.gelu:
+#     M = 64: 2.7, 256: 1.9, 1024: 1.39, 2048: 0.95, 4096: 1.04, 8192: 0.87, 16384: 1.02
+#   down_proj on the stream-K linear (K = 12288, N = 4096):
+#     M = 64: 4.3, 512: 2.0, 1024: 1.47, 2048: 1.24, 3100: 1.00
+#   plain q/o_proj linear (K = N = 4096):
+#     M = 64: 4.2, 256: 3.5, 1024: 2.1, 2048: 1.52, 3100: 1.17, 4096: 1.23
+# The 256 x 256 tiles leave most CUs idle below a few thousand rows, where
+# hipBLASLt picks smaller tiles.  So each site takes its tiled kernel only
+# from the row count where it stops losing (the reference's own rule: fuse a
+# site only where measured faster, integrate.py:80-91): P5 from 256 rows,
+# fc1 + GELU from 2048, the stream-K down_proj from 3072; the plain q/o
+# linear never (None), hipBLASLt being faster at every measured row count.
+# The decode GEMV regime above is separate.
+TILED_MIN_ROWS_MLP = 256
+TILED_MIN_ROWS_GELU_MLP = 2048
+TILED_MIN_ROWS_DOWN = 3072
+TILED_MIN_ROWS_LINEAR: int | None = None
+
+
+def _gemm_rows_ok(x: torch.Tensor, gemv_rows: int, tiled_min: int | None) -> bool:
+    """Row count in one of a site's fused GEMM regimes: the tiled kernel from
+    max(FUSE_MIN_ROWS, tiled_min) rows (never when tiled_min is None), the
+    GEMV up to gemv_rows."""
     rows = _rows(x)
-    return rows >= FUSE_MIN_ROWS or 1 <= rows <= gemv_rows
+    if 1 <= rows <= gemv_rows:
+        return True
+    return tiled_min is not None and rows >= max(FUSE_MIN_ROWS, tiled_min)
 
 
 def _hooked(*mods) -> bool:
@@ -88,10 +115,11 @@ INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
 
 # Per-site choice for the P5 MLP's down_proj, which the reference leaves on
 # the vendor BLAS (integrate.py:80-90, measured a loser on Thor): on MI355X
-# this library's stream-K linear beats hipBLASLt where it applies (fewer
-# output tiles than CUs and a long K loop: at M=3100, K=12288 it ran in
-# 278 us vs 298 us), so the fused MLP uses it for exactly those shapes and
-# the vendor module for every other one.
+# this library's stream-K linear ties or beats hipBLASLt where it applies
+# (fewer output tiles than CUs and a long K loop) from TILED_MIN_ROWS_DOWN
+# rows (at M=3100, K=12288: 283 vs 283 us graph-timed, 286 vs 310 us in
+# bench.py's back-to-back timing), so the fused MLP uses it for exactly those
+# shapes and the vendor module for every other one.
 DOWN_PROJ_STREAM_K = True
 
 # ViT projection site list kept from the reference (integrate.py:95); not
@@ -133,8 +161,8 @@ def _is_p5_mlp(module: nn.Module) -> bool:
 def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """P5-fused replacement: silu(x@Wg)*(x@Wu) in one kernel, then down."""
     wg, wu = self.gate_proj.weight, self.up_proj.weight
-    if (not _gemm_rows_ok(x, GEMV_ROWS_MLP) or not fused_ffn.p5_eligible(x, wg, wu)
-            or grad_needed(x, wg, wu)):
+    if (not _gemm_rows_ok(x, GEMV_ROWS_MLP, TILED_MIN_ROWS_MLP)
+            or not fused_ffn.p5_eligible(x, wg, wu) or grad_needed(x, wg, wu)):
         return _eager(self, x)
     # nn.Linear stores [out, in]; .t() is the free [in, out] view the wrapper
     # takes -- the kernel reads the original weight memory.
@@ -142,7 +170,7 @@ def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     down = self.down_proj
     if _rows(h) < FUSE_MIN_ROWS:
         return _linear(down, h, GEMV_ROWS_DOWN)
-    if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear)
+    if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear) and _rows(h) >= TILED_MIN_ROWS_DOWN
             and linear.linear_eligible(h, down.weight, down.bias)
             and linear.stream_k_planned(h, down.weight)):
         return linear.linear_hip(h, down.weight, down.bias)
@@ -171,9 +199,9 @@ def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
 # ---------------------------------------------------------------------------
 
 def _patched_linear_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    """Route large-M and decode calls to the fused linear (tiled or GEMV);
-    the rows between stay on the vendor BLAS."""
-    if (not _gemm_rows_ok(x, GEMV_ROWS_LINEAR)
+    """Route decode calls (and, where it wins, large-M calls) to the fused
+    linear; the rest stay on the vendor BLAS."""
+    if (not _gemm_rows_ok(x, GEMV_ROWS_LINEAR, TILED_MIN_ROWS_LINEAR)
             or not linear.linear_eligible(x, self.weight, self.bias)
             or grad_needed(x, self.weight, self.bias)):
         return _eager(self, x)
@@ -416,7 +444,8 @@ def _fused_gelu_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     """fc1 + bias + GELU in one kernel (no fc1 output round trip before the
     activation), then fc2 on the vendor BLAS (reference integrate.py:292-303)."""
     fc1, fc2, kind = self._umic_fc
-    if (_rows(x) < FUSE_MIN_ROWS or not linear.linear_eligible(x, fc1.weight, fc1.bias)
+    if (_rows(x) < max(FUSE_MIN_ROWS, TILED_MIN_ROWS_GELU_MLP)
+            or not linear.linear_eligible(x, fc1.weight, fc1.bias)
             or grad_needed(x, fc1.weight, fc1.bias)):
         return _eager(self, x)
     return fc2(linear.linear_hip(x, fc1.weight, fc1.bias, act=kind))
