@@ -128,13 +128,18 @@ def _hf_rms(x, w, eps=1e-6):
 # (op, eager-layout shape): the BASELINE config 2 / 5 norms in the layouts HF
 # calls them with -- LM rows [1, 3100, 4096], the q_norm / k_norm head rows
 # [1, 3100, H, 128] (99200 / 24800 rows), the decode rows ([1, 1, 4096] and
-# 32 / 8 head rows), the ViT rows [16384, 1280] -- and a SigLIP-width LN.
+# 32 / 8 head rows), the ViT rows [16384, 1280] -- a SigLIP-width LN, and
+# batched decode rows (1 to 7 rows of 512 .. 4096).
 EAGER_CASES = [("rmsnorm", (1, 3100, 4096)), ("add_rmsnorm", (1, 3100, 4096)),
                ("rmsnorm", (1, 3100, 32, 128)), ("rmsnorm", (1, 3100, 8, 128)),
                ("rmsnorm", (1, 1, 4096)), ("add_rmsnorm", (1, 1, 4096)),
                ("rmsnorm", (1, 1, 32, 128)), ("rmsnorm", (1, 1, 8, 128)),
                ("layernorm", (16384, 1280)), ("add_layernorm", (16384, 1280)),
-               ("layernorm", (4096, 1152))]
+               ("layernorm", (4096, 1152)),
+               # one to seven rows: 128 .. 512 reducing threads per row
+               ("rmsnorm", (2, 4096)), ("add_rmsnorm", (3, 4096)), ("rmsnorm", (5, 4096)),
+               ("add_rmsnorm", (7, 4096)), ("rmsnorm", (1, 1280)), ("rmsnorm", (3, 1152)),
+               ("add_rmsnorm", (1, 2048)), ("rmsnorm", (6, 512))]
 
 
 @pytest.mark.parametrize("op,shape", EAGER_CASES)

@@ -65,6 +65,8 @@ struct NormArgs {
   float factor;  // RMSNorm: aten MeanOps factor, float(rows) / float(rows * n)
 };
 
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+
 // ---- torch's reduction plan for the RMSNorm statistic (host side) --------
 
 // setReduceConfig (Reduce.cuh) for a contiguous fp32 [rows, n] tensor reduced
@@ -505,6 +507,86 @@ __global__ __launch_bounds__(512) void rms_block_kernel(NormArgs a, RmsPlan p) {
     yr[j] = (uint16_t)f2bf(bf2f(a.w[j]) * rbf(src_val<ADD>(a, row, j) * rstd));
 }
 
+// RMSNorm rows of the plans with 128..512 reducing threads across a row and
+// no split (one to seven rows: the decode steps), with the block kernel's
+// summation order and vector access: thread x holds the 4-element vectors
+// x, x + BW, ... (K4 of them at most) in registers, sums their squares into
+// its four accumulators, and the block reduces as block_x_reduce does --
+// shared-memory halving BW/2 .. 64 (wavefront w + W/2 into w, ...), done by
+// wavefront 0 from one LDS pass, then the in-wavefront tree (offsets 1 .. 32
+// upward; the butterfly gives lane 0 the same sums) -- so two barriers
+// instead of one per halving step.  Requires n % 4 == 0 and 8-byte aligned
+// rows (x, y, w; r and s for the add form).
+template <bool ADD, int BW, int K4>
+__global__ __launch_bounds__(BW) void rms_wide_kernel(NormArgs a) {
+  constexpr int W = BW / kWave;
+  __shared__ float red[BW];
+  __shared__ float stat;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int nv = (int)(a.n / 4);
+  const uint16_t* xr = a.x + row * a.ldx;
+  u32x2 v[K4];
+#pragma unroll
+  for (int k = 0; k < K4; ++k) {
+    const int idx = tid + k * BW;
+    if (idx < nv) v[k] = *reinterpret_cast<const u32x2*>(xr + idx * 4);
+  }
+  if constexpr (ADD) {
+    const uint16_t* rr = a.r + row * a.ldr;
+    uint16_t* sr = a.s + row * a.lds;
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+      const int idx = tid + k * BW;
+      if (idx >= nv) continue;
+      float xf[4], rf[4];
+      unpack4(v[k], xf);
+      unpack4(*reinterpret_cast<const u32x2*>(rr + idx * 4), rf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xf[e] = xf[e] + rf[e];
+      v[k] = pack4(xf);  // bf16(x + r): the eager residual add
+      *reinterpret_cast<u32x2*>(sr + idx * 4) = v[k];
+    }
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < K4; ++k) {
+    if (tid + k * BW >= nv) break;
+    float f[4];
+    unpack4(v[k], f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + f[i] * f[i];
+  }
+  red[tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  __syncthreads();
+  if (tid < kWave) {
+    float r[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) r[w] = red[w * kWave + lane];
+#pragma unroll
+    for (int h = W / 2; h >= 1; h >>= 1)
+#pragma unroll
+      for (int w = 0; w < h; ++w) r[w] = r[w] + r[w + h];
+    const float total = group_sum<kWave>(r[0]);
+    if (tid == 0) stat = rsqrt_cr(total * a.factor + a.eps);
+  }
+  __syncthreads();
+  const float rstd = stat;
+  const uint16_t* wr = a.w;
+  uint16_t* yr = a.y + row * a.ldy;
+#pragma unroll
+  for (int k = 0; k < K4; ++k) {
+    const int idx = tid + k * BW;
+    if (idx >= nv) break;
+    float f[4], wf[4], o[4];
+    unpack4(v[k], f);
+    unpack4(*reinterpret_cast<const u32x2*>(wr + idx * 4), wf);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+    *reinterpret_cast<u32x2*>(yr + idx * 4) = pack4(o);
+  }
+}
+
 // LayerNorm with torch's vectorized kernel order for any n % 4 == 0: 256
 // threads per row, thread t pushes the 4-element vectors t, t + 256, ...; the
 // wavefront tree by shuffle-down (a lane past the end reads itself, as in
@@ -668,6 +750,23 @@ int launch_rms(NormArgs a, hipStream_t st) {
     if (lpr == 16) return launch_rms_lpr<ADD, 16>(a, (int)nvec, (int)vpl, st);
   }
   if (a.rows > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  // the wide rows (one to seven rows) with 8-byte vectors
+  bool wide = p.vec && !p.split && p.bw >= 128 && a.n % 4 == 0 && a.ldx % 4 == 0 &&
+              a.ldy % 4 == 0 && aligned8(a.x) && aligned8(a.y) && aligned8(a.w);
+  if (ADD) wide = wide && a.ldr % 4 == 0 && a.lds % 4 == 0 && aligned8(a.r) && aligned8(a.s);
+  const int64_t k4 = (a.n / 4 + p.bw - 1) / p.bw;
+  if (wide && k4 <= 8) {
+    const dim3 grid((unsigned)a.rows);
+#define UMIC_RMS_WIDE(BW, K)                                                               \
+  if (p.bw == BW && k4 <= K) {                                                              \
+    hipLaunchKernelGGL((rms_wide_kernel<ADD, BW, K>), grid, dim3(BW), 0, st, a);           \
+    return launch_status();                                                                 \
+  }
+    UMIC_RMS_WIDE(512, 2) UMIC_RMS_WIDE(512, 4) UMIC_RMS_WIDE(512, 8)
+    UMIC_RMS_WIDE(256, 2) UMIC_RMS_WIDE(256, 4) UMIC_RMS_WIDE(256, 8)
+    UMIC_RMS_WIDE(128, 2) UMIC_RMS_WIDE(128, 4) UMIC_RMS_WIDE(128, 8)
+#undef UMIC_RMS_WIDE
+  }
   const int threads = p.bw * (p.split ? p.bh : 1);
   hipLaunchKernelGGL((rms_block_kernel<ADD>), dim3((unsigned)a.rows), dim3(threads), 0, st, a,
                      p);
@@ -684,8 +783,6 @@ int launch_ln_rows(const NormArgs& a, int nvec4, hipStream_t st) {
                      nvec4);
   return launch_status();
 }
-
-inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 
 template <bool ADD>
 int launch_ln(const NormArgs& a, hipStream_t st) {
