@@ -489,20 +489,22 @@ def copy_ceiling() -> int:
     import torch
 
     torch.cuda.set_device(0)
-    for moved in (50_798_592, 83_891_200, 167_777_280, 400_000_000):
+    for moved in (50_798_592, 83_891_200, 101_588_992, 167_777_280, 178_257_920,
+                  400_000_000, 2 << 30):
         n = moved // 4  # bf16 elements per side
-        src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(12)]
-        dst = [torch.empty_like(src[0]) for _ in range(12)]
-        for i in range(12):
+        nbuf = 12 if moved < (1 << 30) else 3
+        src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(nbuf)]
+        dst = [torch.empty_like(src[0]) for _ in range(nbuf)]
+        for i in range(nbuf):
             dst[i].copy_(src[i])
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for i in range(12):
+        for i in range(nbuf):
             dst[i].copy_(src[i])
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / 12 * 1e3
+        us = e0.elapsed_time(e1) / nbuf * 1e3
         print(json.dumps({"copy_bytes_moved": moved, "us": round(us, 2),
                           "gbps": round(moved / us / 1e3, 1)}), flush=True)
         del src, dst
