@@ -11,8 +11,9 @@ hooks, and deleting the attribute restores the class forward.
 
 Each replacement forward first decides whether the fused gfx950 kernel
 reproduces the module on the given inputs (GPU bf16 tensors of a handled
-layout; for the GEMM sites also at least FUSE_MIN_ROWS rows, or at most
-the site's GEMV row limit (the decode GEMV); and no
+layout; for the GEMM sites also a row count in one of the site's measured
+regimes -- the tiled kernel from its TILED_MIN_ROWS_* bound (at least
+FUSE_MIN_ROWS), the decode GEMV up to its GEMV_ROWS_* bound; and no
 gradient to carry, since the kernels have no backward).  If not, it runs
 the module's own class forward -- the original eager math on whatever
 device the inputs live on, recorded by autograd as usual.  If the inputs are eligible but libumic_hip.so
@@ -34,11 +35,12 @@ logger = logging.getLogger(__name__)
 
 _SILU_NAMES = ("silu", "swish")
 
-# Below this row count the GEMM motifs run as GEMV (decode, seq=1): the
-# vendor library is the right tool there and the eager intermediates are
-# KB-scale, so the fused GEMMs are only used from this many rows up
-# (reference src/umic/integrate.py:27-30).  Norms and RoPE have no floor:
-# one fused launch always replaces several eager ones.
+# The reference's floor for its tiled GEMM kernels (src/umic/integrate.py:
+# 27-30): below it the eager intermediates are KB-scale and the vendor library
+# runs the GEMMs.  Here it stays the lower bound of every site's tiled regime
+# (each site's own measured bound, TILED_MIN_ROWS_* below, is at least this);
+# the fewest rows take the library's GEMV instead (GEMV_ROWS_*).  Norms and
+# RoPE have no floor: one fused launch always replaces several eager ones.
 FUSE_MIN_ROWS = 64
 
 # ...except for the fewest rows, the decode steps: there the library's entry
