@@ -55,6 +55,7 @@ def _load():
             "orc_set_hw_tables": [P, I64, P],
             "orc_layernorm": [P, P, P, P, P, P, I64, I64, F32, I],
             "orc_add_layernorm": [P, P, P, P, P, P, I64, I64, F32, I],
+            "orc_ln_scalar_stats": [P, P, P, I64, I64, F32, I],
             "orc_rope_text": [P, P, P, P, I64, I64, I64],
             "orc_rope_vision": [P, P, P, P, I64, I64, I64],
             "orc_gemm_nt_f32": [P, P, P, I64, I64, I64],
@@ -62,7 +63,7 @@ def _load():
             "orc_linear": [P, P, P, P, I64, I64, I64, I, I],
         }
         ret = {"orc_rmsnorm", "orc_rms_var", "orc_add_rmsnorm", "orc_layernorm",
-               "orc_add_layernorm"}
+               "orc_add_layernorm", "orc_ln_scalar_stats"}
         for name, args in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -140,36 +141,60 @@ def add_rmsnorm(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float):
 
 def layernorm_torch_order(n: int, aligned: bool = True) -> bool:
     """Whether eager's layer_norm takes its vectorized kernel (the restated
-    Welford order): n % 4 == 0 and an 8-byte aligned contiguous input."""
+    Welford order): n % 4 == 0 and an 8-byte aligned contiguous input.
+    Otherwise it takes its scalar row-moments kernel (order 3)."""
     return n % 4 == 0 and aligned
 
 
 def layernorm(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float,
-              aligned: bool = True, stats: bool = False, _cr_recip: bool = False):
+              aligned: bool = True, stats: bool = False, _cr_recip: bool = False,
+              _exact: bool = False):
     """torch layer_norm of bf16 rows; with stats=True also (mean, rstd).
-    ``_cr_recip`` (tests only) plants a mistake: the torch order with
-    correctly rounded reciprocals instead of gfx950's v_rcp_f32 / v_rsq_f32."""
+    ``aligned=False`` stands for an input eager reads off 8-byte alignment.
+    ``_cr_recip`` and ``_exact`` (tests only) plant mistakes: the vectorized
+    order with correctly rounded reciprocals instead of gfx950's v_rcp_f32 /
+    v_rsq_f32, and exactly rounded statistics instead of eager's order."""
     x, w, b = _u16(x), _u16(w), _u16(b)
     n = x.shape[-1]
     rows = x.size // n
     y = np.empty_like(x)
     mean, rstd = np.empty(rows, np.float32), np.empty(rows, np.float32)
-    order = int(layernorm_torch_order(n, aligned))
-    if order and _cr_recip:
+    order = 1 if layernorm_torch_order(n, aligned) else 3
+    if order == 1 and _cr_recip:
         order = 2
+    if _exact:
+        order = 0
     _check(_load().orc_layernorm(_p(x), _p(w), _p(b), _p(y), _p(mean), _p(rstd), rows, n, eps,
                                  order), "layernorm")
     return (y, mean, rstd) if stats else y
 
 
+def ln_scalar_stats(x: np.ndarray, eps: float, variant: int):
+    """(mean, rstd) of eager's scalar row-moments kernel over bf16 rows in an
+    arithmetic variant (bit flags of orc_ln_scalar_stats; LN_SCALAR_EAGER is
+    eager's, the others are planted mistakes for the tests)."""
+    x = _u16(x)
+    n = x.shape[-1]
+    rows = x.size // n
+    mean, rstd = np.empty(rows, np.float32), np.empty(rows, np.float32)
+    _check(_load().orc_ln_scalar_stats(_p(x), _p(mean), _p(rstd), rows, n, eps, variant),
+           "ln_scalar_stats")
+    return mean, rstd
+
+
+LN_SCALAR_EAGER = 2 | 4 | 16
+
+
 def add_layernorm(x, r, w, b, eps: float):
     """bf16(x + r), then layer_norm of the rounded sum (a fresh, aligned
-    tensor in eager, so the vectorized kernel's order whenever n % 4 == 0)."""
+    tensor in eager: the vectorized kernel's order when n % 4 == 0, the
+    scalar kernel's otherwise)."""
     x, r, w, b = _u16(x), _u16(r), _u16(w), _u16(b)
     n = x.shape[-1]
     normed, summed = np.empty_like(x), np.empty_like(x)
+    order = 1 if layernorm_torch_order(n) else 3
     _check(_load().orc_add_layernorm(_p(x), _p(r), _p(w), _p(b), _p(normed), _p(summed),
-                                     x.size // n, n, eps, int(layernorm_torch_order(n))),
+                                     x.size // n, n, eps, order),
            "add_layernorm")
     return normed, summed
 

@@ -362,11 +362,97 @@ static void ln_stats_torch(const uint16_t* x, int64_t n, float eps, float* mean,
   *rstd = hw_rsq(wv[0].m2 / (float)n + eps);
 }
 
+/* torch-ROCm's other LayerNorm statistics kernel (RowwiseMomentsCUDAKernel),
+ * which eager runs when the vectorized one cannot (n % 4 != 0, or x, w, b
+ * off 8-byte alignment): 512 threads per row (8 wavefronts), thread t folds
+ * elements t, t + 512, ... with WelfordOps::reduce (ATen/native/
+ * SharedReduceOps.h: new_mean = mean + delta / n, m2 += delta * (x -
+ * new_mean)), then cuda_utils::BlockReduce (ATen/native/hip/block_reduce.cuh):
+ * a shuffle-down tree per wavefront with WelfordOps::combine(own, other)
+ * (delta = b.mean - a.mean, nb/n = b.n / (a.n + b.n), mean = a.mean +
+ * delta * nb/n, m2 = a.m2 + b.m2 + delta^2 * a.n * nb/n; an empty side
+ * returns the other), lane 0 of each into shared memory, then the same tree
+ * over the 8 wavefront results (the other 56 lanes the empty identity);
+ * var = m2 / n, rstd = rsqrt(var + eps).  `variant` bits select the
+ * arithmetic forms fitted against eager's recorded statistics:
+ *   1: the reduce's division as fma(delta, v_rcp_f32(n), mean), not a/b
+ *   2: the reduce's m2 term contracted to an fma
+ *   4: the combine's mean and m2 terms contracted to fmas
+ *   8: the combine's nb/n as b.n * v_rcp_f32(n)
+ *  16: rsqrt as v_rsq_f32 (else correctly rounded)
+ *  32: 256 threads per row instead of 512 (a planted mistake) */
+typedef struct {
+  float mean, m2, nf;
+} wfs_t;
+
+static wfs_t wfs_reduce(wfs_t a, float x, int variant) {
+  const float nf = a.nf + 1.0f;
+  const float delta = x - a.mean;
+  const float mean = (variant & 1) ? fmaf(delta, hw_rcp_count(nf), a.mean) : a.mean + delta / nf;
+  const float nd = x - mean;
+  const float m2 = (variant & 2) ? fmaf(delta, nd, a.m2) : a.m2 + delta * nd;
+  return (wfs_t){mean, m2, nf};
+}
+
+static wfs_t wfs_combine(wfs_t a, wfs_t b, int variant) {
+  if (a.nf == 0.0f) return b;
+  if (b.nf == 0.0f) return a;
+  const float delta = b.mean - a.mean;
+  const float cnt = a.nf + b.nf;
+  const float nbn = (variant & 8) ? b.nf * hw_rcp_count(cnt) : b.nf / cnt;
+  float mean, m2;
+  if (variant & 4) {
+    mean = fmaf(delta, nbn, a.mean);
+    m2 = fmaf((delta * delta) * a.nf, nbn, a.m2 + b.m2);
+  } else {
+    mean = a.mean + delta * nbn;
+    m2 = (a.m2 + b.m2) + ((delta * delta) * a.nf) * nbn;
+  }
+  return (wfs_t){mean, m2, cnt};
+}
+
+static void wfs_warp(wfs_t* v, int variant) {  /* 64 lanes, lane 0 keeps the result */
+  for (int off = 32; off > 0; off /= 2)
+    for (int i = 0; i < off; ++i) v[i] = wfs_combine(v[i], v[i + off], variant);
+}
+
+static void ln_stats_torch_scalar(const uint16_t* x, int64_t n, float eps, int variant,
+                                  float* mean, float* rstd) {
+  const int threads = (variant & 32) ? 256 : 512, waves = threads / 64;
+  wfs_t t[512];
+  for (int i = 0; i < threads; ++i) t[i] = (wfs_t){0.0f, 0.0f, 0.0f};
+  for (int64_t j = 0; j < n; ++j) t[j % threads] = wfs_reduce(t[j % threads], bf2f(x[j]), variant);
+  wfs_t s[64];
+  for (int w = 0; w < waves; ++w) {
+    wfs_warp(t + 64 * w, variant);
+    s[w] = t[64 * w];
+  }
+  for (int i = waves; i < 64; ++i) s[i] = (wfs_t){0.0f, 0.0f, 0.0f};
+  wfs_warp(s, variant);
+  *mean = s[0].mean;
+  const float var = s[0].m2 / s[0].nf;
+  *rstd = (variant & 16) ? hw_rsq(var + eps) : rsqrt_cr(var + eps);
+}
+
+/* The forms eager's kernel takes on gfx950 (fitted: every recorded mean and
+ * rstd of the scalar-path fixtures bit for bit): a / b divisions, the
+ * reduce's and the combine's m2 and mean updates contracted, v_rsq_f32. */
+#define LN_SCALAR_EAGER (2 | 4 | 16)
+
+/* Test entry: the statistics above for rows of n, in one of the variants
+ * (LN_SCALAR_EAGER is eager's; the others are planted mistakes). */
+int orc_ln_scalar_stats(const uint16_t* x, float* mean, float* rstd, int64_t rows, int64_t n,
+                        float eps, int variant) {
+  if (!g_rcp_delta || !g_rsq_delta2 || n > g_rcp_n || n <= 0) return -1;
+  g_use_hw = 1;
+  for (int64_t r = 0; r < rows; ++r) ln_stats_torch_scalar(x + r * n, n, eps, variant, mean + r,
+                                                          rstd + r);
+  return 0;
+}
+
 /* Exact statistics (double sums of x and x^2 of bf16 data, rounded once;
- * rsqrt correctly rounded) for rows torch sends down its other LayerNorm
- * kernel (n % 4 != 0 or an input off 8-byte alignment): that kernel's
- * order is not restated, so there the oracle and the library's generic
- * kernel share these statistics and parity with eager is unpinned. */
+ * rsqrt correctly rounded): a planted mistake for the tests, which show that
+ * eager's kernels round differently on some rows. */
 static void ln_stats_exact(const uint16_t* x, int64_t n, float eps, float* mean, float* rstd) {
   double s = 0.0, q = 0.0;
   for (int64_t j = 0; j < n; ++j) {
@@ -388,18 +474,24 @@ static void ln_out(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint
 
 /* torch.nn.functional.layer_norm on bf16 rows with bf16 affine params
  * (nn.LayerNorm in the ViT blocks, HF:283-284).  torch_order 1 selects the
- * vectorized kernel's statistics (needs n % 4 == 0 and the tables), 0 the
- * exact ones; 2 is the Welford order with correctly rounded reciprocals
- * (a planted mistake for the tests).  mean/rstd may be NULL.
+ * vectorized kernel's statistics (needs n % 4 == 0 and the tables), 3 the
+ * scalar kernel's (eager's choice for other widths and misaligned rows),
+ * 0 the exact ones and 2 the vectorized order with correctly rounded
+ * reciprocals (both planted mistakes for the tests).  mean/rstd may be NULL.
  * Reference kernel: kernels/layernorm.py:30-52. */
 int orc_layernorm(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
                   float* mean, float* rstd, int64_t rows, int64_t n, float eps,
                   int torch_order) {
-  if (torch_order && (n % 4 || !g_rcp_delta || !g_rsq_delta2 || n > g_rcp_n)) return -1;
+  if (torch_order == 3) {
+    if (!g_rsq_delta2 || n <= 0) return -1;
+  } else if (torch_order && (n % 4 || !g_rcp_delta || !g_rsq_delta2 || n > g_rcp_n)) {
+    return -1;
+  }
   g_use_hw = torch_order != 2;
   for (int64_t r = 0; r < rows; ++r) {
     float mu, rs;
-    if (torch_order) ln_stats_torch(x + r * n, n, eps, &mu, &rs);
+    if (torch_order == 3) ln_stats_torch_scalar(x + r * n, n, eps, LN_SCALAR_EAGER, &mu, &rs);
+    else if (torch_order) ln_stats_torch(x + r * n, n, eps, &mu, &rs);
     else ln_stats_exact(x + r * n, n, eps, &mu, &rs);
     if (mean) mean[r] = mu;
     if (rstd) rstd[r] = rs;

@@ -43,6 +43,14 @@ RMS_CASES = [(3100, 4096, 0), (99200, 128, 1), (24800, 128, 2), (1, 4096, 3), (2
 LN_CASES = [(16384, 1280, 100), (4096, 1152, 101), (1, 1280, 102), (7, 1280, 103),
             (64, 1280, 104), (100, 4096, 105), (64, 1000, 106), (16390, 128, 107),
             (50, 80, 108), (13, 100, 109), (8, 8192, 110), (3, 4096, 111), (256, 2048, 112)]
+# (rows, n, seed, offset) of the LayerNorm cases eager runs with its scalar
+# kernel (RowwiseMomentsCUDAKernel, then LayerNormForwardCUDAKernel): widths
+# that are not a multiple of 4, and (offset 1) a contiguous input starting one
+# element past an aligned buffer, which defeats the vectorized kernel's
+# alignment check.
+LN_SCALAR_CASES = [(4999, 127, 200, 0), (64, 1001, 201, 0), (7, 6, 202, 0), (13, 130, 203, 0),
+                   (100, 2050, 204, 0), (3, 4097, 205, 0), (257, 1282, 206, 0), (5, 1, 207, 0),
+                   (64, 1280, 208, 1), (9, 4096, 209, 1), (33, 100, 210, 1)]
 KEEP_ROWS = 4  # eager bf16 outputs kept per case (leading rows)
 STAT_ROWS = 1024  # row statistics kept per case (leading rows)
 
@@ -97,6 +105,18 @@ def main(out: str) -> None:
             res[key + "_rstd"] = rstd.view(-1)[:STAT_ROWS].float().cpu().numpy()
             res[key + "_y"] = u16(y[:KEEP_ROWS])
             res[key + "_stat_dtype"] = np.array([str(mean.dtype)])
+            print(key, flush=True)
+
+        for rows, n, seed, off in LN_SCALAR_CASES:
+            x, w, b = draw(rows, n, seed)
+            flat = torch.empty(rows * n + off, dtype=torch.bfloat16, device=dev)
+            flat[off:] = x.to(dev).view(-1)
+            xd = flat[off:].view(rows, n)
+            y, mean, rstd = torch.ops.aten.native_layer_norm(xd, [n], w.to(dev), b.to(dev), eps)
+            key = f"lns_{rows}x{n}_o{off}"
+            res[key + "_mean"] = mean.view(-1)[:STAT_ROWS].float().cpu().numpy()
+            res[key + "_rstd"] = rstd.view(-1)[:STAT_ROWS].float().cpu().numpy()
+            res[key + "_y"] = u16(y[:KEEP_ROWS])
             print(key, flush=True)
 
         # torch.rsqrt over every fp32 mantissa of [1, 4) and a log-uniform

@@ -99,8 +99,8 @@ def test_strided_and_misaligned_rows():
     dm = flat.to(DEV)[1:].view(200, 1280)
     assert dm.data_ptr() % 16 != 0
     y = layernorm.layernorm_hip(dm, wl.to(DEV), bl.to(DEV), 1e-5)
-    # eager's layer_norm takes its row-moments kernel for such a base; the
-    # library takes exact statistics there, as the oracle does with aligned=False
+    # eager's layer_norm takes its scalar row-moments kernel for such a base;
+    # the library follows that kernel's order, as the oracle does with aligned=False
     assert np.array_equal(bits(y), oracle.layernorm(bits(xm), bits(wl), bits(bl), 1e-5,
                                                     aligned=False))
 

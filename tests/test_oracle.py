@@ -375,7 +375,7 @@ def test_reference_smoke_formulas(oracle_lib):
 
 GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 sys.path.insert(0, GOLDEN_DIR)
-from make_eager_gpu import LN_CASES, RMS_CASES, draw  # noqa: E402
+from make_eager_gpu import LN_CASES, LN_SCALAR_CASES, RMS_CASES, draw  # noqa: E402
 
 
 @pytest.fixture(scope="module")
@@ -467,8 +467,53 @@ def test_layernorm_hw_reciprocals_are_needed(oracle_lib, eager_gpu):
     assert np.array_equal(m_t, ref_m) and np.array_equal(r_t, ref_r)
     _, m_cr, r_cr = o.layernorm(xb, bits(w), bits(b), 1e-6, stats=True, _cr_recip=True)
     assert (m_cr != ref_m).sum() > 0 and (r_cr != ref_r).sum() > 0
-    _, m_ex, r_ex = o.layernorm(xb, bits(w), bits(b), 1e-6, aligned=False, stats=True)
+    _, m_ex, r_ex = o.layernorm(xb, bits(w), bits(b), 1e-6, stats=True, _exact=True)
     assert (m_ex != ref_m).sum() > k // 10 and (r_ex != ref_r).sum() > 0
+
+
+@pytest.mark.parametrize("rows,n,seed,off", LN_SCALAR_CASES)
+def test_layernorm_scalar_kernel_matches_eager_gpu(oracle_lib, eager_gpu, rows, n, seed, off):
+    """Widths that are not a multiple of 4, and rows read 2 bytes past
+    alignment (off=1), take eager's scalar row-moments kernel: the oracle's
+    restatement of it gives the recorded mean, rstd and bf16 output bit for
+    bit."""
+    o = oracle_lib
+    x, w, b = draw(rows, n, seed)
+    key = f"lns_{rows}x{n}_o{off}"
+    k = eager_gpu[key + "_mean"].size
+    y, mean, rstd = o.layernorm(bits(x[:k]), bits(w), bits(b), 1e-6, aligned=off == 0,
+                                stats=True)
+    assert np.array_equal(mean, eager_gpu[key + "_mean"])
+    assert np.array_equal(rstd, eager_gpu[key + "_rstd"])
+    yref = eager_gpu[key + "_y"]
+    assert np.array_equal(y[:yref.shape[0]], yref)
+
+
+def test_layernorm_scalar_kernel_forms_are_pinned(oracle_lib, eager_gpu):
+    """Each arithmetic form of the scalar restatement is fixed by the
+    recordings: a correctly rounded rsqrt, an uncontracted Welford update or
+    combine, reciprocal-based divisions, 256 threads per row, or exactly
+    rounded statistics each miss some recorded mean or rstd."""
+    o = oracle_lib
+    eager = o.LN_SCALAR_EAGER
+    planted = {"cr rsqrt": eager & ~16, "plain reduce m2": eager & ~2,
+               "plain combine": eager & ~4, "rcp in reduce": eager | 1,
+               "rcp in combine": eager | 8, "256 threads": eager | 32}
+    misses = {name: 0 for name in list(planted) + ["exact"]}
+    for rows, n, seed, off in LN_SCALAR_CASES:
+        x, w, b = draw(rows, n, seed)
+        key = f"lns_{rows}x{n}_o{off}"
+        k = eager_gpu[key + "_mean"].size
+        ref_m, ref_r = eager_gpu[key + "_mean"], eager_gpu[key + "_rstd"]
+        xb = bits(x[:k])
+        m, r = o.ln_scalar_stats(xb, 1e-6, eager)
+        assert np.array_equal(m, ref_m) and np.array_equal(r, ref_r)
+        for name, v in planted.items():
+            m, r = o.ln_scalar_stats(xb, 1e-6, v)
+            misses[name] += int((m != ref_m).sum() + (r != ref_r).sum())
+        _, m, r = o.layernorm(xb, bits(w), bits(b), 1e-6, stats=True, _exact=True)
+        misses["exact"] += int((m != ref_m).sum() + (r != ref_r).sum())
+    assert all(v > 0 for v in misses.values()), misses
 
 
 def test_gfx950_tables_shape_and_scale():

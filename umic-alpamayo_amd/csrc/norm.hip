@@ -22,8 +22,9 @@
 //             across the four wavefronts; count reciprocals are v_rcp_f32,
 //             rstd is v_rsq_f32(m2 / n + eps), and the fused products are
 //             the ones the ROCm build contracts.  Rows torch sends to its
-//             other LayerNorm kernel (n % 4 != 0, a contiguous input off
-//             8-byte alignment) take exact statistics here instead.
+//             scalar LayerNorm kernel (n % 4 != 0, or x, weight or bias
+//             off 8-byte alignment) follow that kernel's order instead:
+//             512 reducing threads per row, IEEE divisions, v_rsq_f32.
 //
 // Layouts.  The register paths keep each row in registers, so a row is read
 // once and written once:
@@ -632,38 +633,76 @@ __global__ __launch_bounds__(256) void ln_torch_block_kernel(NormArgs a) {
   }
 }
 
-// LayerNorm rows torch sends down its other kernel (n % 4 != 0, or a
-// contiguous input off 8-byte alignment): its order is not reproduced, so
-// these take exact statistics -- double sums of x and x^2 of bf16 data, exact
-// whatever the order, each rounded once to fp32; rsqrt correctly rounded.
-__device__ double block_sum(double v, double* red) {
-  v = group_sum<kWave>(v);
-  const int wid = threadIdx.x / kWave;
-  __syncthreads();  // `red` may still be read from a previous reduction
-  if ((threadIdx.x & (kWave - 1)) == 0) red[wid] = v;
-  __syncthreads();
-  double t = 0.0;
-  for (int i = 0; i < (int)(blockDim.x / kWave); ++i) t += red[i];
-  return t;
+// LayerNorm rows eager sends down its scalar kernel (n % 4 != 0, or x,
+// weight or bias off 8-byte alignment) in that kernel's order
+// (RowwiseMomentsCUDAKernel, layer_norm_kernel.cu): 512 reducing threads per
+// row, thread t folding elements t, t + 512, ... by Welford updates with IEEE
+// divisions; a shuffle-down tree per 64-thread group; the same tree over the
+// 8 group results; var = m2 / n, rstd by v_rsq_f32.  Here one wavefront
+// takes a row: lane l carries the states of reducing threads l + 64 v
+// (v = 0..7) side by side and runs the 8 group trees together, so a short
+// row costs one wavefront rather than a 512-thread block.
+struct Ws {
+  float mean, m2, nf;
+};
+
+// WelfordOps::combine (SharedReduceOps.h): an empty side yields the other;
+// the mean and m2 updates contract to fmas on gfx950.
+__device__ __forceinline__ Ws ws_combine(Ws a, Ws b) {
+  if (a.nf == 0.0f) return b;
+  if (b.nf == 0.0f) return a;
+  const float delta = b.mean - a.mean;
+  const float cnt = a.nf + b.nf;
+  const float nbn = b.nf / cnt;
+  return Ws{__builtin_fmaf(delta, nbn, a.mean),
+            __builtin_fmaf((delta * delta) * a.nf, nbn, a.m2 + b.m2), cnt};
 }
 
 template <bool ADD>
-__global__ __launch_bounds__(256) void ln_exact_block_kernel(NormArgs a) {
-  __shared__ double red[256 / kWave];
-  const int64_t row = blockIdx.x;
-  write_sum<ADD>(a, row);
-  const double inv_n = 1.0 / (double)a.n;
-  double sum = 0.0, ssq = 0.0;
-  for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x) {
-    const float f = src_val<ADD>(a, row, j);
-    sum += (double)f;
-    ssq += (double)(f * f);
+__global__ __launch_bounds__(256) void ln_scalar_rows_kernel(NormArgs a) {
+  const int lane = (int)threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  Ws s[8];
+  int cnt[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    s[v] = Ws{0.0f, 0.0f, 0.0f};
+    cnt[v] = 0;
   }
-  const double mean_d = block_sum(sum, red) * inv_n;
-  const float mean = (float)mean_d;
-  const float rstd = rsqrt_cr((float)(block_sum(ssq, red) * inv_n - mean_d * mean_d) + a.eps);
+  for (int64_t j0 = 0; j0 < a.n; j0 += 512) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int64_t j = j0 + 64 * v + lane;
+      if (j < a.n) {
+        const float f = src_val<ADD>(a, row, j);
+        if constexpr (ADD) a.s[row * a.lds + j] = (uint16_t)f2bf(f);
+        const float nf = (float)++cnt[v];
+        const float delta = f - s[v].mean;
+        const float mean = s[v].mean + delta / nf;
+        s[v] = Ws{mean, __builtin_fmaf(delta, f - mean, s[v].m2), nf};
+      }
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const Ws o{__shfl_down(s[v].mean, off, kWave), __shfl_down(s[v].m2, off, kWave),
+                 __shfl_down(s[v].nf, off, kWave)};
+      s[v] = ws_combine(s[v], o);
+    }
+  }
+  // lane 0 holds the 8 group results; in eager's second tree offsets 32..8
+  // pair them with empty lanes (no change), offsets 4, 2, 1 pair v, v + off
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1)
+#pragma unroll
+    for (int v = 0; v < off; ++v) s[v] = ws_combine(s[v], s[v + off]);
+  const float mean = __shfl(s[0].mean, 0, kWave);
+  const float var = __shfl(s[0].m2, 0, kWave) / __shfl(s[0].nf, 0, kWave);
+  const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
   uint16_t* yr = a.y + row * a.ldy;
-  for (int64_t j = threadIdx.x; j < a.n; j += blockDim.x) {
+  for (int64_t j = lane; j < a.n; j += kWave) {
     const float f = src_val<ADD>(a, row, j);
     yr[j] = (uint16_t)f2bf(__builtin_fmaf(bf2f(a.w[j]), rstd * (f - mean), bf2f(a.b[j])));
   }
@@ -794,8 +833,8 @@ int launch_ln(const NormArgs& a, hipStream_t st) {
   const bool torch_vec = a.n % 4 == 0 && a.n <= (1 << 24) && aligned8(a.w) && aligned8(a.b) &&
                          (ADD || !contiguous || aligned8(a.x));
   if (!torch_vec) {
-    hipLaunchKernelGGL((ln_exact_block_kernel<ADD>), dim3((unsigned)a.rows), dim3(256), 0, st,
-                       a);
+    hipLaunchKernelGGL((ln_scalar_rows_kernel<ADD>), dim3((unsigned)((a.rows + 3) / 4)),
+                       dim3(256), 0, st, a);
     return launch_status();
   }
   bool vec = a.ldx % 4 == 0 && a.ldy % 4 == 0 && aligned8(a.x) && aligned8(a.y);
