@@ -87,14 +87,16 @@ def test_text_rope_contiguous_and_batched():
     assert torch.equal(qo1, rq1) and torch.equal(ko1, rk1)
 
 
-def test_text_rope_unaligned_tables_take_the_staged_path():
+@pytest.mark.parametrize("S,Hq,Hk,D", [(300, 8, 2, 128), (20, 2, 1, 1024)])
+def test_text_rope_unaligned_tables_take_the_staged_path(S, Hq, Hk, D):
     """bf16 tables are read per item with 16-byte loads when their bases and
     row strides allow it; tables at an odd element offset (2-byte aligned
-    rows) are staged through LDS instead -- same results either way."""
+    rows) are staged through LDS instead -- by the lane-per-chunk kernel when
+    a head row fits a wavefront (D = 128), else by the item-pair kernel
+    (D = 1024).  Same results every way."""
     from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
 
     g = torch.Generator().manual_seed(2)
-    S, Hq, Hk, D = 300, 8, 2, 128
     cos, sin = text_tables(S, D, 1e6)
     q = bf16_randn(1, S, Hq, D, gen=g).to(DEV).transpose(1, 2)
     k = bf16_randn(1, S, Hk, D, gen=g).to(DEV).transpose(1, 2)
@@ -147,3 +149,55 @@ def test_vision_rope_bf16_tables_and_fallback_wrapper():
     qo, ko = fused(q, k, cos, sin)
     rq, rk = apply_rotary_pos_emb_vision(q, k, cos, sin)
     assert torch.equal(qo, rq) and torch.equal(ko, rk)
+
+
+@pytest.mark.parametrize("S,H,D,cs_pad", [(37, 3, 16, 0), (50, 5, 32, 0), (19, 4, 48, 1),
+                                          (64, 2, 96, 0), (23, 7, 112, 1), (11, 2, 256, 0),
+                                          (9, 3, 512, 0), (300, 16, 80, 1), (1, 1, 80, 0)])
+def test_vision_rope_lane_form_vs_oracle(S, H, D, cs_pad):
+    """Head rows that fit a wavefront (D / 8 <= 64 chunks) take the
+    lane-per-chunk kernel: 60 or 64 lanes per wavefront hold whole rows, the
+    rotation partner D / 16 lanes away is fetched across lanes.  fp32 table
+    rows 16-byte aligned (vector staging) or D + 1 floats apart (cs_pad:
+    scalar staging).  Bit for bit with the oracle and with HF on the GPU."""
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb_vision
+
+    print(f"vision lane form S={S} H={H} D={D} cs_pad={cs_pad}", flush=True)
+    g = torch.Generator().manual_seed(S * 31 + D)
+    qkv = bf16_randn(S, 3, H, D, gen=g)
+    ang = 3.0 * torch.randn(S, D, generator=g)
+    cbig = torch.zeros(S, D + cs_pad)
+    sbig = torch.zeros(S, D + cs_pad)
+    cbig[:, :D], sbig[:, :D] = ang.cos(), ang.sin()
+    c, s_ = cbig.to(DEV)[:, :D], sbig.to(DEV)[:, :D]
+    q, k, _ = qkv.to(DEV).permute(1, 0, 2, 3).unbind(0)
+    qo, ko = rope.apply_rotary_vision_hip(q, k, c, s_)
+    torch.cuda.synchronize()
+    qc, kc, _ = qkv.permute(1, 0, 2, 3).unbind(0)
+    cn, sn = cbig[:, :D].contiguous().numpy(), sbig[:, :D].contiguous().numpy()
+    assert np.array_equal(bits(qo), oracle.rope_vision(bits(qc), cn, sn))
+    assert np.array_equal(bits(ko), oracle.rope_vision(bits(kc), cn, sn))
+    rq, rk = apply_rotary_pos_emb_vision(q, k, c, s_)
+    assert torch.equal(qo, rq) and torch.equal(ko, rk)
+
+
+def test_text_rope_lane_form_batched_staged_tables():
+    """Batched text RoPE whose bf16 tables are staged (odd element offset)
+    through the lane-per-chunk kernel, with a per-batch and a broadcast
+    table: positions of both batches inside one block's table rows."""
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
+
+    g = torch.Generator().manual_seed(3)
+    B, S, Hq, Hk, D = 2, 7, 3, 1, 64
+    cos, sin = text_tables(S, D, 1e6, B=B, offsets=(0, 40))
+    q = bf16_randn(B, S, Hq, D, gen=g).to(DEV).transpose(1, 2)
+    k = bf16_randn(B, S, Hk, D, gen=g).to(DEV).transpose(1, 2)
+    for bsel in (slice(0, 2), slice(0, 1)):
+        cb, sb = cos[bsel], sin[bsel]
+        cbig = torch.zeros(cb.shape[0], S, D + 1, dtype=torch.bfloat16, device=DEV)
+        sbig = torch.zeros_like(cbig)
+        cbig[..., 1:] = cb.to(DEV)
+        sbig[..., 1:] = sb.to(DEV)
+        qo, ko = rope.apply_rotary_text_hip(q, k, cbig[..., 1:], sbig[..., 1:])
+        rq, rk = apply_rotary_pos_emb(q, k, cb.to(DEV), sb.to(DEV))
+        assert torch.equal(qo, rq) and torch.equal(ko, rk), bsel

@@ -2,24 +2,31 @@
 //
 //   out[d]        = x[d]        * cos[d]        - x[d + D/2] * sin[d]
 //   out[d + D/2]  = x[d + D/2]  * cos[d + D/2]  + x[d]       * sin[d + D/2]
-// (HF rotate_half convention).  A work item owns one head row's pair of
-// VEC-element chunks, [c*VEC, c*VEC+VEC) and the same chunk shifted by D/2,
-// so both halves of every rotation pair are in the same lane: no partner
-// gather, no cross-lane traffic.  Consecutive items walk the chunks of a
-// head, then the heads of a position, so each load/store instruction of a
-// wavefront covers whole contiguous head rows of q (then k).
+// (HF rotate_half convention).  Two work layouts:
+//   item pair  -- a work item owns one head row's pair of VEC-element
+//                 chunks, [c*VEC, c*VEC+VEC) and the same chunk shifted by
+//                 D/2, so both halves of every rotation pair are in the same
+//                 lane.  Consecutive items walk the chunks of a head, then
+//                 the heads of a position.  Each instruction covers one half
+//                 of several head rows: whole 128-byte lines when D/2 is 64
+//                 elements (text, D = 128), half-used lines otherwise.
+//   lane chunk -- (16-byte chunks, D/8 <= 64) a lane owns one contiguous
+//                 chunk, a wavefront whole head rows, and the rotation
+//                 partner comes from the lane D/16 away: every instruction
+//                 covers one contiguous run.  Vision (D = 80, 160-byte rows)
+//                 runs 33 against 40 us in the item-pair form.
 //
 // Tables.  cos/sin are read once from HBM for q AND k (the reference's
 // per-tensor launches read them twice).  fp32 tables (vision) are staged
-// into LDS per block: one block serves a flat range of 1024 items (4 per
-// thread, all loads in flight together), stages the cos/sin rows of the
-// positions it touches, and rotates every item from registers.  bf16 tables
-// (text, [S, 128] = 0.8 MB each, L2-resident) are instead read per item
-// straight from global -- 16 bytes per half, the same width as the item --
-// with 512 items per block: measured 8% faster than staging (no staging
-// loop, no barrier), while for fp32 tables the per-item reads would be 4x
-// the item's own bytes and staging wins.  Activations are streamed with
-// non-temporal loads: each element is read once and written once.
+// into LDS per block: the block stages the cos/sin rows of the positions its
+// range touches, and rotates every item from registers.  bf16 tables (text,
+// [S, 128] = 0.8 MB each, L2-resident) are instead read per item straight
+// from global in the item-pair form -- 16 bytes per half, the same width as
+// the item -- with 512 items per block: measured 8% faster than staging (no
+// staging loop, no barrier), and 10% faster than the lane-chunk form with
+// staged tables.  For fp32 tables the per-item reads would be 4x the item's
+// own bytes and staging wins.  Activations are streamed with non-temporal
+// loads: each element is read once and written once.
 //
 // Arithmetic modes (no fp contraction anywhere in this library):
 //   TEXT   -- every op rounds to bf16, as the eager bf16 chain does:
@@ -241,6 +248,137 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb, int n
       Chunk<VEC>::store(os[u] + dl, ol);
       Chunk<VEC>::store(os[u] + dh, oh);
     }
+  }
+}
+
+// Lane-per-chunk form for 16-byte chunks when a head row (D/8 chunks) fits
+// a wavefront.  A lane owns ONE contiguous chunk: a wavefront's L lanes (the
+// largest multiple of D/8 up to 64) hold L/(D/8) whole head rows, so each
+// load and store instruction covers one contiguous run of rows -- where the
+// item-pair form above covers the two halves of every row with two
+// instructions, each touching twice the cache lines (for D = 80 the halves
+// are 80-byte pieces of 160-byte rows).  The rotation partner, the chunk
+// D/2 elements away in the same row, is D/16 lanes away: fetched with a
+// cross-lane permute.  cos/sin rows of the positions a block touches are
+// staged in LDS once per block; every chunk at column 8t reads table
+// elements 8t .. 8t + 7 of its position.  kLaneItems chunks per lane, all
+// loads issued before the staging barrier.
+constexpr int kLaneItems = 4;
+
+template <int MODE, bool CS32, bool CS_VEC>
+__global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int L, int np_max) {
+  extern __shared__ float4 tables_v[];  // float4: 16-byte aligned rows
+  float* const tables_l = reinterpret_cast<float*>(tables_v);
+  const int D = (int)a.D;
+  float* const cs_l = tables_l;
+  float* const sn_l = tables_l + np_max * D;
+  const int lane = (int)threadIdx.x & (kWave - 1);
+  const int wave = (int)threadIdx.x / kWave;
+  const int cph = a.chunks.d;  // chunks per head row
+  const int cpp = a.ipp.d;     // chunks per position
+  const int64_t npos = a.B * a.S;
+  const int64_t total = npos * cpp;
+  const int64_t b0 = (int64_t)blockIdx.x * (4 * L * kLaneItems);
+  const int64_t p0 = b0 / cpp;
+  const int r0 = (int)(b0 - p0 * cpp);
+
+  const uint16_t* xs[kLaneItems];
+  uint16_t* os[kLaneItems];
+  u32x4 xv[kLaneItems];
+  int tofs[kLaneItems], tcol[kLaneItems];
+  bool ok[kLaneItems];
+#pragma unroll
+  for (int u = 0; u < kLaneItems; ++u) {
+    const int off = (wave * kLaneItems + u) * L + lane;
+    ok[u] = lane < L && b0 + off < total;
+    int r, t;
+    const int pp = div_small(a.ipp, ok[u] ? r0 + off : r0, r);
+    const int head = div_small(a.chunks, r, t);
+    const int64_t p = p0 + pp;
+    int64_t b = 0, sidx = p;
+    if (a.B != 1) {
+      b = p / a.S;
+      sidx = p - b * a.S;
+    }
+    if (head < a.Hq) {
+      xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + head * a.q_sh + t * 8;
+      os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + head * a.qo_sh + t * 8;
+    } else {
+      const int h = head - (int)a.Hq;
+      xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh + t * 8;
+      os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh + t * 8;
+    }
+    tofs[u] = pp * D + t * 8;
+    tcol[u] = t;
+  }
+#pragma unroll
+  for (int u = 0; u < kLaneItems; ++u) xv[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u]));
+
+  // stage the touched positions' rows (bf16 tables widen exactly)
+  const int np = (int)(npos - p0 < np_max ? npos - p0 : np_max);
+  if constexpr (CS_VEC) {  // fp32 rows, 16-byte aligned: one float4 per thread and table
+    for (int i = (int)threadIdx.x; i < 2 * np * (D / 4); i += blockDim.x) {
+      const int which = i >= np * (D / 4);
+      const int j = which ? i - np * (D / 4) : i;
+      int d4;
+      const int pp = div_small(a.dim, j * 4, d4);
+      const int64_t p = p0 + pp;
+      int64_t b = 0, sidx = p;
+      if (a.B != 1) {
+        b = p / a.S;
+        sidx = p - b * a.S;
+      }
+      const float* src = static_cast<const float*>(which ? a.sin : a.cos);
+      *reinterpret_cast<float4*>((which ? sn_l : cs_l) + j * 4) =
+          *reinterpret_cast<const float4*>(src + b * a.cs_sb + sidx * a.cs_ss + d4);
+    }
+  } else {
+    for (int i = (int)threadIdx.x; i < np * D; i += blockDim.x) {
+      int d;
+      const int pp = div_small(a.dim, i, d);
+      const int64_t p = p0 + pp;
+      int64_t b = 0, sidx = p;
+      if (a.B != 1) {
+        b = p / a.S;
+        sidx = p - b * a.S;
+      }
+      const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+      if constexpr (CS32) {
+        cs_l[i] = static_cast<const float*>(a.cos)[off];
+        sn_l[i] = static_cast<const float*>(a.sin)[off];
+      } else {
+        cs_l[i] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+        sn_l[i] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+      }
+    }
+  }
+  __syncthreads();
+
+  const int hs = cph / 2;  // partner distance in lanes
+#pragma unroll
+  for (int u = 0; u < kLaneItems; ++u) {
+    const bool low = tcol[u] < hs;
+    const int src = ok[u] ? (low ? lane + hs : lane - hs) : lane;
+    u32x4 pv;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pv[w] = (uint32_t)__shfl((int)xv[u][w], src, kWave);
+    float x[8], xp[8], c[8], sn[8], o[8];
+    unpack8(xv[u], x);
+    unpack8(pv, xp);
+    const float4* cp = reinterpret_cast<const float4*>(cs_l + tofs[u]);
+    const float4* sp = reinterpret_cast<const float4*>(sn_l + tofs[u]);
+    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
+    c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+    sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
+    sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float rot = low ? -xp[e] : xp[e];  // rotate_half: (-x_hi, x_lo)
+      if constexpr (MODE == UMIC_ROPE_TEXT) o[e] = rbf(x[e] * c[e]) + rbf(rot * sn[e]);
+      else o[e] = x[e] * c[e] + rot * sn[e];
+    }
+    if (ok[u]) *reinterpret_cast<u32x4*>(os[u]) = pack8(o);
   }
 }
 
@@ -532,8 +670,46 @@ RopeArgs with_divisors(const RopeArgs& a) {
   return b;
 }
 
+// LDS budget of the lane-per-chunk form's two staged tables
+constexpr size_t kLanesMaxLds = 48 * 1024;
+
+// The lane-per-chunk form (16-byte chunks, a head row within a wavefront),
+// or UMIC_ERR_UNSUPPORTED when it does not apply.
+template <int MODE, bool CS32>
+int launch_lanes(const RopeArgs& a0, hipStream_t st) {
+  const int64_t cph = a0.D / 8;
+  if (a0.D % 16 != 0 || cph > kWave) return UMIC_ERR_UNSUPPORTED;
+  RopeArgs a = a0;
+  a.chunks = small_div((int)cph);
+  a.ipp = small_div((int)((a.Hq + a.Hk) * cph));
+  a.dim = small_div((int)a.D);
+  const int64_t npos = a.B * a.S;
+  const int64_t cpp = (a.Hq + a.Hk) * cph;
+  const int L = (int)(kWave / cph * cph);
+  const int64_t cpb = (int64_t)4 * L * kLaneItems;
+  // a block's cpb chunks touch at most cpb / cpp + 2 positions
+  const int64_t np_max = std::min<int64_t>(cpb / cpp + 2, npos);
+  const size_t lds = (size_t)(2 * np_max * a.D) * sizeof(float);
+  if (lds > kLanesMaxLds) return UMIC_ERR_UNSUPPORTED;
+  const int64_t blocks = (npos * cpp + cpb - 1) / cpb;
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  const bool cs_vec = CS32 && a.cs_sb % 4 == 0 && a.cs_ss % 4 == 0 &&
+                      (uintptr_t)a.cos % 16 == 0 && (uintptr_t)a.sin % 16 == 0;
+  if (cs_vec)
+    hipLaunchKernelGGL((rope_lanes_kernel<MODE, CS32, true>), dim3((unsigned)blocks), dim3(256),
+                       lds, st, a, L, (int)np_max);
+  else
+    hipLaunchKernelGGL((rope_lanes_kernel<MODE, CS32, false>), dim3((unsigned)blocks),
+                       dim3(256), lds, st, a, L, (int)np_max);
+  return launch_status();
+}
+
 template <int MODE, bool CS32, int VEC>
 int launch_staged(const RopeArgs& a0, hipStream_t st) {
+  if constexpr (VEC == 8) {
+    const int rc = launch_lanes<MODE, CS32>(a0, st);
+    if (rc != UMIC_ERR_UNSUPPORTED) return rc;
+  }
   const RopeArgs a = with_divisors<VEC>(a0);
   const int64_t npos = a.B * a.S;
   const int64_t ipp = (a.Hq + a.Hk) * (a.D / 2 / VEC);
