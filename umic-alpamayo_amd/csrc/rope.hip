@@ -11,9 +11,9 @@
 //                 of several head rows: whole 128-byte lines when D/2 is 64
 //                 elements (text, D = 128), half-used lines otherwise.
 //   lane chunk -- (16-byte chunks, D/8 <= 64) a lane owns one contiguous
-//                 chunk, a wavefront whole head rows, and the rotation
-//                 partner comes from the lane D/16 away: every instruction
-//                 covers one contiguous run.  Vision (D = 80, 160-byte rows)
+//                 chunk, a wavefront whole head rows (low halves in lanes
+//                 0..31, high halves in 32..63), and the rotation partner
+//                 is lane ^ 32: every instruction covers one contiguous run.  Vision (D = 80, 160-byte rows)
 //                 runs 33 against 40 us in the item-pair form.
 //
 // Tables.  cos/sin are read once from HBM for q AND k (the reference's
@@ -252,76 +252,91 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb, int n
 }
 
 // Lane-per-chunk form for 16-byte chunks when a head row (D/8 chunks) fits
-// a wavefront.  A lane owns ONE contiguous chunk: a wavefront's L lanes (the
-// largest multiple of D/8 up to 64) hold L/(D/8) whole head rows, so each
-// load and store instruction covers one contiguous run of rows -- where the
-// item-pair form above covers the two halves of every row with two
-// instructions, each touching twice the cache lines (for D = 80 the halves
-// are 80-byte pieces of 160-byte rows).  The rotation partner, the chunk
-// D/2 elements away in the same row, is D/16 lanes away: fetched with a
-// cross-lane permute.  cos/sin rows of the positions a block touches are
-// staged in LDS once per block; every chunk at column 8t reads table
-// elements 8t .. 8t + 7 of its position.  kLaneItems chunks per lane, all
-// loads issued before the staging barrier.
+// a wavefront.  A lane owns ONE contiguous chunk: the low-half chunks of a
+// wavefront's hpw head rows sit in lanes 0..31 (row r's chunk c at lane
+// r*hh + c, hh = D/16 chunks per half), their high-half partners in the same
+// places of lanes 32..63.  Each load and store instruction then covers the
+// hpw rows whole -- one contiguous run -- where the item-pair form above
+// covers the two halves of every row with two instructions, each touching
+// twice the cache lines (for D = 80 the halves are 80-byte pieces of
+// 160-byte rows).  The rotation partner is lane ^ 32, swapped in by
+// v_permlane32_swap (VALU, no LDS).  cos/sin rows of the positions a block
+// touches are staged in LDS once per block; a chunk at column 8t reads table
+// elements 8t .. 8t + 7 of its position, stored in cs_slot's 12-float chunk
+// slots so the chunks of a row one instruction reads sit in distinct banks.
+// kLaneItems row groups per wavefront, all loads issued before the staging
+// barrier.
 constexpr int kLaneItems = 4;
 
 template <int MODE, bool CS32, bool CS_VEC>
-__global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int L, int np_max) {
+__global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, int np_max) {
   extern __shared__ float4 tables_v[];  // float4: 16-byte aligned rows
   float* const tables_l = reinterpret_cast<float*>(tables_v);
   const int D = (int)a.D;
+  const int rs = cs_row(D);  // a multiple of 12 floats: rows stay 16-byte aligned
   float* const cs_l = tables_l;
-  float* const sn_l = tables_l + np_max * D;
+  float* const sn_l = tables_l + np_max * rs;
   const int lane = (int)threadIdx.x & (kWave - 1);
   const int wave = (int)threadIdx.x / kWave;
-  const int cph = a.chunks.d;  // chunks per head row
-  const int cpp = a.ipp.d;     // chunks per position
+  const bool upper = lane >= 32;
+  int tt;
+  const int hw = div_small(a.chunks, lane & 31, tt);  // row within the group, chunk in half
+  const int hh = a.chunks.d;                          // chunks per half row
+  const int t = tt + (upper ? hh : 0);                // chunk within the row
+  const int hpp = a.ipp.d;                            // head rows per position
   const int64_t npos = a.B * a.S;
-  const int64_t total = npos * cpp;
-  const int64_t b0 = (int64_t)blockIdx.x * (4 * L * kLaneItems);
-  const int64_t p0 = b0 / cpp;
-  const int r0 = (int)(b0 - p0 * cpp);
+  const int64_t nrows = npos * hpp;
+  const int rpb = 4 * kLaneItems * hpw;  // head rows per block
+  const int64_t b0 = (int64_t)blockIdx.x * rpb;
+  const int64_t p0 = b0 / hpp;
+  const int r0 = (int)(b0 - p0 * hpp);
 
-  const uint16_t* xs[kLaneItems];
   uint16_t* os[kLaneItems];
   u32x4 xv[kLaneItems];
-  int tofs[kLaneItems], tcol[kLaneItems];
+  int tofs[kLaneItems];
   bool ok[kLaneItems];
 #pragma unroll
   for (int u = 0; u < kLaneItems; ++u) {
-    const int off = (wave * kLaneItems + u) * L + lane;
-    ok[u] = lane < L && b0 + off < total;
-    int r, t;
-    const int pp = div_small(a.ipp, ok[u] ? r0 + off : r0, r);
-    const int head = div_small(a.chunks, r, t);
+    const int off = (wave * kLaneItems + u) * hpw + hw;
+    ok[u] = hw < hpw && b0 + off < nrows;
+    int head;
+    const int pp = div_small(a.ipp, ok[u] ? r0 + off : r0, head);
     const int64_t p = p0 + pp;
     int64_t b = 0, sidx = p;
     if (a.B != 1) {
       b = p / a.S;
       sidx = p - b * a.S;
     }
+    const uint16_t* xs;
     if (head < a.Hq) {
-      xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + head * a.q_sh + t * 8;
+      xs = a.q + b * a.q_sb + sidx * a.q_ss + head * a.q_sh + t * 8;
       os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + head * a.qo_sh + t * 8;
     } else {
       const int h = head - (int)a.Hq;
-      xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh + t * 8;
+      xs = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh + t * 8;
       os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh + t * 8;
     }
-    tofs[u] = pp * D + t * 8;
-    tcol[u] = t;
+    xv[u] = ld_stream(reinterpret_cast<const u32x4*>(xs));
+    tofs[u] = pp * rs + cs_slot(t * 8);
   }
-#pragma unroll
-  for (int u = 0; u < kLaneItems; ++u) xv[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u]));
 
   // stage the touched positions' rows (bf16 tables widen exactly)
   const int np = (int)(npos - p0 < np_max ? npos - p0 : np_max);
-  if constexpr (CS_VEC) {  // fp32 rows, 16-byte aligned: one float4 per thread and table
-    for (int i = (int)threadIdx.x; i < 2 * np * (D / 4); i += blockDim.x) {
-      const int which = i >= np * (D / 4);
-      const int j = which ? i - np * (D / 4) : i;
+  if constexpr (CS_VEC) {
+    // fp32 rows, 16-byte aligned: float4 copies.  Chunk C (8 floats) of the
+    // staged rows sits at slot 12 C, its halves at +0 and +4 floats.  Each
+    // 16-lane group writes the same half of 16 consecutive chunks, whose
+    // slots 12 C cover the 64 banks once each.
+    const int nc = np * (D / 8);
+    const int ncp = (nc + 15) & ~15;
+    for (int i = (int)threadIdx.x; i < 4 * ncp; i += blockDim.x) {
+      const int which = i >= 2 * ncp;
+      const int k = which ? i - 2 * ncp : i;
+      const int h = (k >> 4) & 1;
+      const int C = (k >> 5) * 16 + (k & 15);
+      if (C >= nc) continue;
       int d4;
-      const int pp = div_small(a.dim, j * 4, d4);
+      const int pp = div_small(a.dim, C * 8 + 4 * h, d4);
       const int64_t p = p0 + pp;
       int64_t b = 0, sidx = p;
       if (a.B != 1) {
@@ -329,7 +344,7 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int L, int 
         sidx = p - b * a.S;
       }
       const float* src = static_cast<const float*>(which ? a.sin : a.cos);
-      *reinterpret_cast<float4*>((which ? sn_l : cs_l) + j * 4) =
+      *reinterpret_cast<float4*>((which ? sn_l : cs_l) + 12 * C + 4 * h) =
           *reinterpret_cast<const float4*>(src + b * a.cs_sb + sidx * a.cs_ss + d4);
     }
   } else {
@@ -343,25 +358,27 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int L, int 
         sidx = p - b * a.S;
       }
       const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d;
+      const int slot = pp * rs + cs_slot(d);
       if constexpr (CS32) {
-        cs_l[i] = static_cast<const float*>(a.cos)[off];
-        sn_l[i] = static_cast<const float*>(a.sin)[off];
+        cs_l[slot] = static_cast<const float*>(a.cos)[off];
+        sn_l[slot] = static_cast<const float*>(a.sin)[off];
       } else {
-        cs_l[i] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
-        sn_l[i] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
+        cs_l[slot] = bf2f(static_cast<const uint16_t*>(a.cos)[off]);
+        sn_l[slot] = bf2f(static_cast<const uint16_t*>(a.sin)[off]);
       }
     }
   }
   __syncthreads();
 
-  const int hs = cph / 2;  // partner distance in lanes
 #pragma unroll
   for (int u = 0; u < kLaneItems; ++u) {
-    const bool low = tcol[u] < hs;
-    const int src = ok[u] ? (low ? lane + hs : lane - hs) : lane;
+    // the partner chunk (lane ^ 32): every lane takes part in the swap
     u32x4 pv;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) pv[w] = (uint32_t)__shfl((int)xv[u][w], src, kWave);
+    for (int w = 0; w < 4; ++w) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(xv[u][w], xv[u][w], false, false);
+      pv[w] = upper ? sw[0] : sw[1];
+    }
     float x[8], xp[8], c[8], sn[8], o[8];
     unpack8(xv[u], x);
     unpack8(pv, xp);
@@ -374,7 +391,7 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int L, int 
     sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float rot = low ? -xp[e] : xp[e];  // rotate_half: (-x_hi, x_lo)
+      const float rot = upper ? xp[e] : -xp[e];  // rotate_half: (-x_hi, x_lo)
       if constexpr (MODE == UMIC_ROPE_TEXT) o[e] = rbf(x[e] * c[e]) + rbf(rot * sn[e]);
       else o[e] = x[e] * c[e] + rot * sn[e];
     }
@@ -677,30 +694,30 @@ constexpr size_t kLanesMaxLds = 48 * 1024;
 // or UMIC_ERR_UNSUPPORTED when it does not apply.
 template <int MODE, bool CS32>
 int launch_lanes(const RopeArgs& a0, hipStream_t st) {
-  const int64_t cph = a0.D / 8;
-  if (a0.D % 16 != 0 || cph > kWave) return UMIC_ERR_UNSUPPORTED;
+  const int64_t hh = a0.D / 16;  // chunks per half row
+  if (a0.D % 16 != 0 || hh > 32) return UMIC_ERR_UNSUPPORTED;
   RopeArgs a = a0;
-  a.chunks = small_div((int)cph);
-  a.ipp = small_div((int)((a.Hq + a.Hk) * cph));
+  a.chunks = small_div((int)hh);
+  a.ipp = small_div((int)(a.Hq + a.Hk));
   a.dim = small_div((int)a.D);
   const int64_t npos = a.B * a.S;
-  const int64_t cpp = (a.Hq + a.Hk) * cph;
-  const int L = (int)(kWave / cph * cph);
-  const int64_t cpb = (int64_t)4 * L * kLaneItems;
-  // a block's cpb chunks touch at most cpb / cpp + 2 positions
-  const int64_t np_max = std::min<int64_t>(cpb / cpp + 2, npos);
-  const size_t lds = (size_t)(2 * np_max * a.D) * sizeof(float);
+  const int64_t hpp = a.Hq + a.Hk;
+  const int hpw = (int)(32 / hh);  // head rows per wavefront
+  const int64_t rpb = (int64_t)4 * kLaneItems * hpw;
+  // a block's rpb head rows touch at most rpb / hpp + 2 positions
+  const int64_t np_max = std::min<int64_t>(rpb / hpp + 2, npos);
+  const size_t lds = (size_t)(2 * np_max * cs_row((int)a.D)) * sizeof(float);
   if (lds > kLanesMaxLds) return UMIC_ERR_UNSUPPORTED;
-  const int64_t blocks = (npos * cpp + cpb - 1) / cpb;
+  const int64_t blocks = (npos * hpp + rpb - 1) / rpb;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   const bool cs_vec = CS32 && a.cs_sb % 4 == 0 && a.cs_ss % 4 == 0 &&
                       (uintptr_t)a.cos % 16 == 0 && (uintptr_t)a.sin % 16 == 0;
   if (cs_vec)
     hipLaunchKernelGGL((rope_lanes_kernel<MODE, CS32, true>), dim3((unsigned)blocks), dim3(256),
-                       lds, st, a, L, (int)np_max);
+                       lds, st, a, hpw, (int)np_max);
   else
     hipLaunchKernelGGL((rope_lanes_kernel<MODE, CS32, false>), dim3((unsigned)blocks),
-                       dim3(256), lds, st, a, L, (int)np_max);
+                       dim3(256), lds, st, a, hpw, (int)np_max);
   return launch_status();
 }
 
