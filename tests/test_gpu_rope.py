@@ -91,16 +91,17 @@ def test_text_rope_contiguous_and_batched():
 def test_text_rope_unaligned_tables_take_the_staged_path(S, Hq, Hk, D):
     """bf16 tables are read per item with 16-byte loads when their bases and
     row strides allow it; tables at an odd element offset (2-byte aligned
-    rows) are staged through LDS instead -- by the lane-per-chunk kernel when
-    a head row fits a wavefront (D = 128), else by the item-pair kernel
-    (D = 1024).  Same results every way."""
+    rows) or 4 elements in (8-byte aligned: staged with 8-byte moves) are
+    staged through LDS instead -- by the lane-per-chunk kernel when a head
+    row fits a wavefront (D = 128), else by the item-pair kernel (D = 1024).
+    Same results every way."""
     from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
 
     g = torch.Generator().manual_seed(2)
     cos, sin = text_tables(S, D, 1e6)
     q = bf16_randn(1, S, Hq, D, gen=g).to(DEV).transpose(1, 2)
     k = bf16_randn(1, S, Hk, D, gen=g).to(DEV).transpose(1, 2)
-    for shift in (0, 1):
+    for shift in (0, 1, 4):
         cbig = torch.zeros(1, S, D + 8, dtype=torch.bfloat16, device=DEV)
         sbig = torch.zeros_like(cbig)
         cbig[..., shift:shift + D] = cos.to(DEV)

@@ -15,6 +15,7 @@ constexpr int kWave = 64;
 // Native 16-byte vector (clang ext_vector) -- the unit of every coalesced
 // global access below (one global_load/store_dwordx4 per lane).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));  // 8-byte accesses
 
 // ---- bf16 <-> fp32 --------------------------------------------------------
 // bf16 values travel as raw 16-bit patterns packed two per 32-bit word

@@ -273,8 +273,6 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int
 
 // ---- register path: LayerNorm --------------------------------------------
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 // Word 3 of a raw buffer resource (the one gemm.hip uses): untyped dword
 // access with range checking against num_records.
 constexpr int kRsrcWord3 = 0x00020000;

@@ -23,8 +23,8 @@
 // [S, 128] = 0.8 MB each, L2-resident) are instead read per item straight
 // from global in the item-pair form -- 16 bytes per half, the same width as
 // the item -- with 512 items per block: measured 8% faster than staging (no
-// staging loop, no barrier), and 10% faster than the lane-chunk form with
-// staged tables.  For fp32 tables the per-item reads would be 4x the item's
+// staging loop, no barrier), and as fast as the lane-chunk form with staged
+// tables (15.3-16.5 against 15.9-17.0 us at q[1,32,3100,128]).  For fp32 tables the per-item reads would be 4x the item's
 // own bytes and staging wins.  Activations are streamed with non-temporal
 // loads: each element is read once and written once.
 //
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, in
   // stage the touched positions' rows (bf16 tables widen exactly)
   const int np = (int)(npos - p0 < np_max ? npos - p0 : np_max);
   if constexpr (CS_VEC) {
-    // fp32 rows, 16-byte aligned: float4 copies.  Chunk C (8 floats) of the
+    // rows aligned for 4-element moves (fp32: 16 bytes, bf16: 8).  Chunk C (8 floats) of the
     // staged rows sits at slot 12 C, its halves at +0 and +4 floats.  Each
     // 16-lane group writes the same half of 16 consecutive chunks, whose
     // slots 12 C cover the 64 banks once each.
@@ -343,9 +343,17 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, in
         b = p / a.S;
         sidx = p - b * a.S;
       }
-      const float* src = static_cast<const float*>(which ? a.sin : a.cos);
-      *reinterpret_cast<float4*>((which ? sn_l : cs_l) + 12 * C + 4 * h) =
-          *reinterpret_cast<const float4*>(src + b * a.cs_sb + sidx * a.cs_ss + d4);
+      const int64_t off = b * a.cs_sb + sidx * a.cs_ss + d4;
+      float4 v;
+      if constexpr (CS32) {
+        v = *reinterpret_cast<const float4*>(static_cast<const float*>(which ? a.sin : a.cos) +
+                                             off);
+      } else {  // bf16 rows, 8-byte aligned halves, widened exactly
+        const u32x2 w = *reinterpret_cast<const u32x2*>(
+            static_cast<const uint16_t*>(which ? a.sin : a.cos) + off);
+        v = float4{bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y)};
+      }
+      *reinterpret_cast<float4*>((which ? sn_l : cs_l) + 12 * C + 4 * h) = v;
     }
   } else {
     for (int i = (int)threadIdx.x; i < np * D; i += blockDim.x) {
@@ -710,8 +718,9 @@ int launch_lanes(const RopeArgs& a0, hipStream_t st) {
   if (lds > kLanesMaxLds) return UMIC_ERR_UNSUPPORTED;
   const int64_t blocks = (npos * hpp + rpb - 1) / rpb;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  const bool cs_vec = CS32 && a.cs_sb % 4 == 0 && a.cs_ss % 4 == 0 &&
-                      (uintptr_t)a.cos % 16 == 0 && (uintptr_t)a.sin % 16 == 0;
+  const uintptr_t cs_align = CS32 ? 16 : 8;
+  const bool cs_vec = a.cs_sb % 4 == 0 && a.cs_ss % 4 == 0 &&
+                      (uintptr_t)a.cos % cs_align == 0 && (uintptr_t)a.sin % cs_align == 0;
   if (cs_vec)
     hipLaunchKernelGGL((rope_lanes_kernel<MODE, CS32, true>), dim3((unsigned)blocks), dim3(256),
                        lds, st, a, hpw, (int)np_max);
