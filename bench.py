@@ -38,7 +38,9 @@ over the norm/RoPE ops as for the GPU; cpu_oracle = the scalar C oracle (one
 core) on a bounded quarter-row sample of the norm/RoPE workload.
 layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
 prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
-HIP graph); --no-layer skips it.  kv_cache = text RoPE fused with the
+HIP graph); vit_encoder = BASELINE config 4 in context, the Qwen3-VL vision
+encoder (4 blocks, 16384 tokens, hidden 1280) eager vs with the vision
+fusions injected; --no-layer skips both.  kv_cache = text RoPE fused with the
 in-place KV-cache append against RoPE + two slice copies, at prefill and at a
 32-token flow step; --no-kv-cache skips it.
 """
@@ -626,6 +628,74 @@ def layer_step() -> dict:
     return res
 
 
+def vit_step(reps: int = 10) -> dict:
+    """BASELINE config 4 in context: the Qwen3-VL vision encoder at the ViT
+    width of the norm/RoPE rows (hidden 1280, 16 heads, head_dim 80, MLP
+    1280 -> 5120 with the tanh GELU, 4 blocks, a deepstack tap after block 1)
+    on 16 images of 32 x 32 patches -- 16384 tokens, the [16384, 1280]
+    LayerNorm and [16384, 16, 80] vision-RoPE rows -- with random weights
+    (LayerNorm affine 1 + N(0, 0.1) / N(0, 0.1)).  Timed eager, then with
+    fuse_layernorms, fuse_vision_rope, fuse_vision_encoder_pipeline and
+    fuse_gelu_mlps injected (the reference's vision set,
+    src/umic/optimize.py:120-140, plus the fc1 + GELU epilogue)."""
+    import torch
+    from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionModel
+
+    from umic import integrate
+
+    cfg = Qwen3VLVisionConfig(depth=4, hidden_size=1280, num_heads=16, intermediate_size=5120,
+                              hidden_act="gelu_pytorch_tanh", patch_size=16,
+                              temporal_patch_size=2, in_channels=3, spatial_merge_size=2,
+                              out_hidden_size=2048, num_position_embeddings=2304,
+                              deepstack_visual_indexes=[1], attn_implementation="sdpa")
+    torch.manual_seed(0)
+    m = Qwen3VLVisionModel(cfg)
+    inv_freq = m.rotary_pos_emb.inv_freq.clone()
+    m = m.to(torch.bfloat16)
+    # a bf16 checkpoint keeps this fp32 buffer (HF builds it in fp32), so
+    # cos/sin reach the RoPE in fp32, as in the model
+    m.rotary_pos_emb.inv_freq = inv_freq
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, torch.nn.LayerNorm):
+                mod.weight.add_(0.1 * torch.randn_like(mod.weight))
+                mod.bias.add_(0.1 * torch.randn_like(mod.bias))
+    m = m.to("cuda").eval()
+    grid = torch.tensor([[1, 32, 32]] * 16, device="cuda")
+    px = torch.randn(16 * 32 * 32, 3 * 2 * 16 * 16, device="cuda").to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps  # ms
+
+    res = {"tokens": 16384, "blocks": 4}
+    with torch.no_grad():
+        run = lambda: m(px, grid_thw=grid)  # noqa: E731
+        ref = run().last_hidden_state
+        res["encoder_eager_ms"] = round(timed(run), 3)
+        integrate.fuse_layernorms(m)
+        integrate.fuse_vision_rope()
+        integrate.fuse_vision_encoder_pipeline(m)
+        integrate.fuse_gelu_mlps(m)
+        try:
+            out = run().last_hidden_state
+            res["encoder_umic_ms"] = round(timed(run), 3)
+            res["max_rel_err"] = round(float((out.float() - ref.float()).abs().max()
+                                             / ref.float().abs().max()), 5)
+        finally:
+            integrate.unfuse_rope()
+    return res
+
+
 def kv_cache_step(reps: int = 20) -> dict:
     """Text RoPE fused with the in-place KV-cache append
     (umic_rope_kv_append_bf16) against the chain it replaces -- this
@@ -778,7 +848,8 @@ def main() -> int:
     ap.add_argument("--decode-layer", action="store_true",
                     help="run ten fused config-5 decode steps (for a kernel trace) and exit")
     ap.add_argument("--no-layer", action="store_true",
-                    help="skip the decoder-layer (config 5) prefill/decode timing")
+                    help="skip the decoder-layer (config 5) and vision-encoder (config 4) "
+                         "timings")
     ap.add_argument("--no-kv-cache", action="store_true",
                     help="skip the fused RoPE + KV-cache append timing")
     args = ap.parse_args()
@@ -885,6 +956,7 @@ def main() -> int:
         "kernels": kern,
         "roofline": roof,
         "layer": None if args.no_layer else layer_step(),
+        "vit_encoder": None if args.no_layer else vit_step(),
         "kv_cache": None if args.no_kv_cache else kv_cache_step(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_reference(args.cpu_budget_s),
         "cpu_oracle": None if args.no_cpu_baseline else cpu_oracle(args.cpu_sample_s),

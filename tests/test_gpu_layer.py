@@ -153,7 +153,11 @@ def test_config1_mlp_block(call_log):
     assert call_log["umic_gate_silu_mul_bf16"] == 2       # the block's MLP, then p5
 
 
-def test_vision_pipeline_on_gpu(call_log):
+@pytest.mark.parametrize("fp32_rotary", [False, True])
+def test_vision_pipeline_on_gpu(call_log, fp32_rotary):
+    """The vision encoder with every vision fusion injected.  With the whole
+    model cast to bf16 the rotary tables are bf16; a bf16 checkpoint keeps
+    the rotary inv_freq buffer fp32 (fp32_rotary), and cos/sin arrive fp32."""
     from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLVisionConfig
     from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLVisionModel
 
@@ -163,7 +167,11 @@ def test_vision_pipeline_on_gpu(call_log):
                               num_position_embeddings=2304, deepstack_visual_indexes=[1],
                               attn_implementation="sdpa")
     torch.manual_seed(0)
-    m = Qwen3VLVisionModel(cfg).to(torch.bfloat16)
+    m = Qwen3VLVisionModel(cfg)
+    inv_freq = m.rotary_pos_emb.inv_freq.clone()
+    m = m.to(torch.bfloat16)
+    if fp32_rotary:
+        m.rotary_pos_emb.inv_freq = inv_freq
     with torch.no_grad():
         for mod in m.modules():
             if isinstance(mod, torch.nn.LayerNorm):

@@ -13,8 +13,10 @@
 //   lane chunk -- (16-byte chunks, D/8 <= 64) a lane owns one contiguous
 //                 chunk, a wavefront whole head rows (low halves in lanes
 //                 0..31, high halves in 32..63), and the rotation partner
-//                 is lane ^ 32: every instruction covers one contiguous run.  Vision (D = 80, 160-byte rows)
-//                 runs 33 against 40 us in the item-pair form.
+//                 is lane ^ 32: every instruction covers one contiguous run.
+//                 Used whenever D is not a multiple of 128: vision (D = 80,
+//                 160-byte rows) runs 33 against 40 us in the item-pair
+//                 form.
 //
 // Tables.  cos/sin are read once from HBM for q AND k (the reference's
 // per-tensor launches read them twice).  fp32 tables (vision) are staged
@@ -757,9 +759,19 @@ int launch_staged(const RopeArgs& a0, hipStream_t st) {
 }
 
 // direct_ok: the bf16 tables allow 16-byte reads (aligned bases, row
-// strides multiples of 8 elements); otherwise they are staged.
+// strides multiples of 8 elements); otherwise they are staged.  The
+// item-pair forms are kept for head dims whose half rows are whole 128-byte
+// lines (D a multiple of 128); any other D with 16-byte chunks takes the
+// lane-chunk form (at D = 80 with bf16 tables 33-37 against 38-41 us, at
+// text D = 64 9.5 against 14.4-15.3 us).
 template <int MODE, bool CS32, int VEC>
 int launch_rope(const RopeArgs& a, bool direct_ok, hipStream_t st) {
+  if constexpr (VEC == 8) {
+    if (a.D % 128 != 0) {
+      const int rc = launch_lanes<MODE, CS32>(a, st);
+      if (rc != UMIC_ERR_UNSUPPORTED) return rc;
+    }
+  }
   if constexpr (!CS32 && VEC == 8) {
     if (!direct_ok) return launch_staged<MODE, CS32, VEC>(a, st);
     const int64_t nitems = a.B * a.S * (a.Hq + a.Hk) * (a.D / 2 / VEC);
