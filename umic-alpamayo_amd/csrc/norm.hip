@@ -167,7 +167,9 @@ __device__ __forceinline__ Wf wf_step(Wf s, bool upper) {
 // lane (e.g. the [S*H, 128] per-head q/k norms) leave a wavefront only 1-2 KB
 // of loads in flight, too little to cover HBM latency; a group then takes
 // RPG consecutive rows and issues all their loads before reducing any.
-template <bool ADD, int LPR, int MAXV, int RPG>
+// FULL: every lane's MAXV slots hold vectors of the row (nvec == MAXV * LPR,
+// vpl == MAXV), so the per-slot liveness tests are compile-time true.
+template <bool ADD, int LPR, int MAXV, int RPG, bool FULL = false>
 __global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int vpl) {
   const int rows_per_block = (int)blockDim.x / LPR * RPG;
   const int lane = threadIdx.x & (LPR - 1);
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int c = i * LPR + lane;
-    live[i] = i < vpl && c < nvec;
+    live[i] = FULL || (i < vpl && c < nvec);
     cix[i] = live[i] ? c : 0;
   }
   bool rlive[RPG];
@@ -301,7 +303,11 @@ __device__ __forceinline__ u32x2 pack4(const float f[4]) {
 // Loads and stores are 8-byte chunks, 128 contiguous bytes per group, through
 // buffer resources over the wavefront's four rows.  The pushes take their
 // count reciprocals from a table of v_rcp_f32 results.
-template <bool ADD, int M4>
+// FULL: the row fills every slot (n = 256 * M4, as the ViT width 1280 with
+// M4 = 5), so the per-slot guards are compile-time true.  Without them the
+// launch at [16384, 1280] measured 16.4-17.2 against 17.6-18.6 us: the
+// statistics between a row's loads and its stores are on the critical path.
+template <bool ADD, int M4, bool FULL = false>
 __global__ __launch_bounds__(256) void ln_rows_kernel(NormArgs a, int nvec4) {
   constexpr int G = 16, M = 4 * M4, kRowsPerWave = kWave / G;
   constexpr int kNt = 2;  // buffer access cache policy: non-temporal (streamed once)
@@ -341,7 +347,8 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(NormArgs a, int nvec4) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) xf[e] = xf[e] + rf[e];
       xv[m] = pack4(xf);  // bf16(x + r): the eager residual add
-      if (16 * m + l < nvec4) __builtin_amdgcn_raw_buffer_store_b64(xv[m], sr, ls + 128 * m, 0, kNt);
+      if (FULL || 16 * m + l < nvec4)
+        __builtin_amdgcn_raw_buffer_store_b64(xv[m], sr, ls + 128 * m, 0, kNt);
     }
   }
 
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(NormArgs a, int nvec4) {
 #pragma unroll
       for (int j = 0; 4 * w + k + 16 * j < M; ++j) {
         const int m = 4 * w + k + 16 * j;
-        if (16 * m + l >= nvec4) break;  // a thread's vectors are a prefix of j
+        if (!FULL && 16 * m + l >= nvec4) break;  // a thread's vectors are a prefix of j
         float f[4];
         unpack4(xv[m], f);
 #pragma unroll
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(NormArgs a, int nvec4) {
   const int ly = (int)(rw * a.ldy * 2) + l * 8;
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    if (16 * m + l >= nvec4) continue;
+    if (!FULL && 16 * m + l >= nvec4) continue;
     float f[4], wf[4], bf[4], o[4];
     unpack4(xv[m], f);
     unpack4(__builtin_amdgcn_raw_buffer_load_b64(wr, l * 8 + 128 * m, 0, 0), wf);
@@ -723,8 +730,12 @@ int launch_rms_rows(const NormArgs& a, int nvec, int vpl, hipStream_t st) {
   const int rows_per_block = threads / LPR * RPG;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((rms_rows_kernel<ADD, LPR, MAXV, RPG>), dim3((unsigned)blocks),
-                     dim3(threads), 0, st, a, nvec, vpl);
+  if (vpl == MAXV && nvec == MAXV * LPR)
+    hipLaunchKernelGGL((rms_rows_kernel<ADD, LPR, MAXV, RPG, true>), dim3((unsigned)blocks),
+                       dim3(threads), 0, st, a, nvec, vpl);
+  else
+    hipLaunchKernelGGL((rms_rows_kernel<ADD, LPR, MAXV, RPG, false>), dim3((unsigned)blocks),
+                       dim3(threads), 0, st, a, nvec, vpl);
   return launch_status();
 }
 
@@ -816,8 +827,12 @@ int launch_ln_rows(const NormArgs& a, int nvec4, hipStream_t st) {
   const int rows_per_block = threads / 16;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((ln_rows_kernel<ADD, M4>), dim3((unsigned)blocks), dim3(threads), 0, st, a,
-                     nvec4);
+  if (nvec4 == 64 * M4)
+    hipLaunchKernelGGL((ln_rows_kernel<ADD, M4, true>), dim3((unsigned)blocks), dim3(threads), 0,
+                       st, a, nvec4);
+  else
+    hipLaunchKernelGGL((ln_rows_kernel<ADD, M4, false>), dim3((unsigned)blocks), dim3(threads), 0,
+                       st, a, nvec4);
   return launch_status();
 }
 
