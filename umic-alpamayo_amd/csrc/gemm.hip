@@ -750,7 +750,11 @@ struct GemvJob {
   int count;
 };
 
-template <int NB, int ACT, bool BIAS, int MR>
+// FULL: K is a whole number of passes (every slab of every pass is inside
+// K: K a multiple of 2048 U, as 4096 and 12288), so the per-slab bounds
+// tests are compile-time true -- a branch inside the streaming loop.
+// Bit-identical; 1-2% faster at the config-5 decode sites.
+template <int NB, int ACT, bool BIAS, int MR, bool FULL = false>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
   int si = 0;  // launch-uniform per workgroup
 #pragma unroll
@@ -792,7 +796,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
     u32x4 wv[U][NB][R], xv[U][MR];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + 64 * u < chunks ? c0 + 64 * u : c0;  // c0 < chunks
+      const int64_t c = FULL || c0 + 64 * u < chunks ? c0 + 64 * u : c0;  // c0 < chunks
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -803,7 +807,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c0 + 64 * u >= chunks) break;
+      if (!FULL && c0 + 64 * u >= chunks) break;
       float xf[MR][8];
 #pragma unroll
       for (int m = 0; m < MR; ++m) unpack8(xv[u][m], xf[m]);
@@ -869,19 +873,28 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvJob job) {
   }
 }
 
+template <int NB, int ACT, bool BIAS, int MR>
+void launch_gemv_mr(const GemvJob& job, dim3 gd, dim3 bd, hipStream_t st) {
+  constexpr int64_t pass = (int64_t)2048 * (MR >= 8 ? 1 : 2);  // K per pass of the waves
+  if (job.K % pass == 0)
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, MR, true>), gd, bd, 0, st, job);
+  else
+    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, MR, false>), gd, bd, 0, st, job);
+}
+
 template <int NB, int ACT, bool BIAS>
 int launch_gemv_job(const GemvJob& job, hipStream_t st) {
   const int64_t grid = job.first[job.count];
   if (grid <= 0 || grid > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
   const dim3 gd((unsigned)grid), bd(kGemvWaves * 64);
   if (job.M <= 1)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 1>), gd, bd, 0, st, job);
+    launch_gemv_mr<NB, ACT, BIAS, 1>(job, gd, bd, st);
   else if (job.M <= 2)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 2>), gd, bd, 0, st, job);
+    launch_gemv_mr<NB, ACT, BIAS, 2>(job, gd, bd, st);
   else if (job.M <= 4)
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 4>), gd, bd, 0, st, job);
+    launch_gemv_mr<NB, ACT, BIAS, 4>(job, gd, bd, st);
   else
-    hipLaunchKernelGGL((gemv_kernel<NB, ACT, BIAS, 8>), gd, bd, 0, st, job);
+    launch_gemv_mr<NB, ACT, BIAS, 8>(job, gd, bd, st);
   return launch_status();
 }
 
