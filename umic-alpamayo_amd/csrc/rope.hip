@@ -270,8 +270,25 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb, int n
 // barrier.
 constexpr int kLaneItems = 4;
 
+template <int MODE, bool CS32, bool CS_VEC, bool FULL>
+__device__ __forceinline__ void lanes_block(const RopeArgs& a, int hpw, int np_max);
+
+// Lanes past the wavefront's hpw rows (lane & 31 >= hpw * hh, e.g. 2 + 2 of
+// 64 at D = 80) repeat the last row's chunks: they and their partners load,
+// rotate and store exactly what the owning lanes do, so no lane needs a store
+// guard; with every row of the block in range (all blocks but the last) the
+// block runs without guards.
 template <int MODE, bool CS32, bool CS_VEC>
 __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, int np_max) {
+  const int64_t nrows = a.B * a.S * a.ipp.d;
+  if ((int64_t)(blockIdx.x + 1) * (4 * kLaneItems * hpw) <= nrows)
+    lanes_block<MODE, CS32, CS_VEC, true>(a, hpw, np_max);
+  else
+    lanes_block<MODE, CS32, CS_VEC, false>(a, hpw, np_max);
+}
+
+template <int MODE, bool CS32, bool CS_VEC, bool FULL>
+__device__ __forceinline__ void lanes_block(const RopeArgs& a, int hpw, int np_max) {
   extern __shared__ float4 tables_v[];  // float4: 16-byte aligned rows
   float* const tables_l = reinterpret_cast<float*>(tables_v);
   const int D = (int)a.D;
@@ -282,7 +299,8 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, in
   const int wave = (int)threadIdx.x / kWave;
   const bool upper = lane >= 32;
   int tt;
-  const int hw = div_small(a.chunks, lane & 31, tt);  // row within the group, chunk in half
+  const int hw_l = div_small(a.chunks, lane & 31, tt);  // row within the group, chunk in half
+  const int hw = hw_l < hpw ? hw_l : hpw - 1;           // spare lanes repeat the last row
   const int hh = a.chunks.d;                          // chunks per half row
   const int t = tt + (upper ? hh : 0);                // chunk within the row
   const int hpp = a.ipp.d;                            // head rows per position
@@ -300,7 +318,7 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, in
 #pragma unroll
   for (int u = 0; u < kLaneItems; ++u) {
     const int off = (wave * kLaneItems + u) * hpw + hw;
-    ok[u] = hw < hpw && b0 + off < nrows;
+    ok[u] = FULL || b0 + off < nrows;
     int head;
     const int pp = div_small(a.ipp, ok[u] ? r0 + off : r0, head);
     const int64_t p = p0 + pp;
@@ -405,7 +423,7 @@ __global__ __launch_bounds__(256) void rope_lanes_kernel(RopeArgs a, int hpw, in
       if constexpr (MODE == UMIC_ROPE_TEXT) o[e] = rbf(x[e] * c[e]) + rbf(rot * sn[e]);
       else o[e] = x[e] * c[e] + rot * sn[e];
     }
-    if (ok[u]) *reinterpret_cast<u32x4*>(os[u]) = pack8(o);
+    if (FULL || ok[u]) *reinterpret_cast<u32x4*>(os[u]) = pack8(o);
   }
 }
 
