@@ -23,6 +23,7 @@ Capture never decides results: a step that cannot be captured runs eagerly.
 from __future__ import annotations
 
 import functools
+import gc
 import logging
 from typing import Any, Callable
 
@@ -48,12 +49,26 @@ def _on_side_stream(fn: Callable[[], Any]):
 
 def _capture(fn: Callable[[], Any], pool=None, warm: bool = True):
     """Capture one call of fn in a new graph, after one warm-up call on a
-    side stream unless ``warm`` is False; returns (graph, outputs)."""
+    side stream unless ``warm`` is False; returns (graph, outputs).
+
+    Python's cyclic garbage collector is held off while the capture is open.
+    A collection there finalizes whatever dead cycles exist at that moment --
+    a discarded runner is one (the model's forward holds the runner, which
+    holds the model) -- and so destroys their graphs and releases their graph
+    memory pools inside another stream capture, which HIP does not allow (the
+    process aborted that way).  torch.cuda.graph no longer collects before a
+    capture by default, so the guard is here."""
     if warm:
         _on_side_stream(fn)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, pool=pool):
-        out = fn()
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, pool=pool):
+            out = fn()
+    finally:
+        if was_enabled:
+            gc.enable()
     return graph, out
 
 
