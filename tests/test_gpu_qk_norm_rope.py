@@ -44,6 +44,7 @@ SHAPES = [
     (1, 9, 3, 1, 128),         # a ragged last block
     (1, 5, 2, 1, 256),         # 16 lanes per head row: the full-row DPP mirror
     (1, 300, 16, 4, 256),      # D = 256 at many rows
+    (3, 7, 12, 4, 128),        # four rows per thread, batch of three, ragged last block
 ]
 
 

@@ -2,14 +2,19 @@
 //
 //   out[d]        = x[d]        * cos[d]        - x[d + D/2] * sin[d]
 //   out[d + D/2]  = x[d + D/2]  * cos[d + D/2]  + x[d]       * sin[d + D/2]
-// (HF rotate_half convention).  Two work layouts:
-//   item pair  -- a work item owns one head row's pair of VEC-element
-//                 chunks, [c*VEC, c*VEC+VEC) and the same chunk shifted by
-//                 D/2, so both halves of every rotation pair are in the same
-//                 lane.  Consecutive items walk the chunks of a head, then
-//                 the heads of a position.  Each instruction covers one half
-//                 of several head rows: whole 128-byte lines when D/2 is 64
-//                 elements (text, D = 128), half-used lines otherwise.
+// (HF rotate_half convention).  Three work layouts:
+//   head group -- (bf16 tables read from global, 16-byte chunks, D a
+//                 multiple of 128) a thread owns chunk c of R head rows of
+//                 one position: the chunk pair [8c, 8c+8) and the same chunk
+//                 shifted by D/2 of each row, so both halves of every
+//                 rotation pair are in the same lane, and the position's
+//                 cos/sin chunks are loaded once for R rows.  Consecutive
+//                 threads walk the chunks, then the head groups, then the
+//                 positions; at D = 128 each instruction covers whole
+//                 128-byte half rows.
+//   item pair  -- (staged tables, or 4- / 2-byte chunks) a work item owns
+//                 one head row's chunk pair as above; consecutive items walk
+//                 the chunks of a head, then the heads of a position.
 //   lane chunk -- (16-byte chunks, D/8 <= 64) a lane owns one contiguous
 //                 chunk, a wavefront whole head rows (low halves in lanes
 //                 0..31, high halves in 32..63), and the rotation partner
@@ -22,13 +27,13 @@
 // per-tensor launches read them twice).  fp32 tables (vision) are staged
 // into LDS per block: the block stages the cos/sin rows of the positions its
 // range touches, and rotates every item from registers.  bf16 tables (text,
-// [S, 128] = 0.8 MB each, L2-resident) are instead read per item straight
-// from global in the item-pair form -- 16 bytes per half, the same width as
-// the item -- with 512 items per block: measured 8% faster than staging (no
-// staging loop, no barrier), and as fast as the lane-chunk form with staged
-// tables (15.3-16.5 against 15.9-17.0 us at q[1,32,3100,128]).  For fp32 tables the per-item reads would be 4x the item's
-// own bytes and staging wins.  Activations are streamed with non-temporal
-// loads: each element is read once and written once.
+// [S, 128] = 0.8 MB each, L2-resident) are instead read straight from
+// global by the head-group form -- 16 bytes per half, once per R rows: as
+// fast as the lane-chunk form with staged tables already with one row per
+// thread (15.3-16.5 against 15.9-17.0 us at q[1,32,3100,128]), with no
+// staging loop and no barrier.  For fp32 tables the per-row reads would be
+// 4x the row's own bytes and staging wins.  Activations are streamed with
+// non-temporal loads: each element is read once and written once.
 //
 // Arithmetic modes (no fp contraction anywhere in this library):
 //   TEXT   -- every op rounds to bf16, as the eager bf16 chain does:
@@ -258,8 +263,8 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(RopeArgs a, int ipb, int n
 // wavefront's hpw head rows sit in lanes 0..31 (row r's chunk c at lane
 // r*hh + c, hh = D/16 chunks per half), their high-half partners in the same
 // places of lanes 32..63.  Each load and store instruction then covers the
-// hpw rows whole -- one contiguous run -- where the item-pair form above
-// covers the two halves of every row with two instructions, each touching
+// hpw rows whole -- one contiguous run -- where the head-group and
+// item-pair forms above cover the two halves of every row with two instructions, each touching
 // twice the cache lines (for D = 80 the halves are 80-byte pieces of
 // 160-byte rows).  The rotation partner is lane ^ 32, swapped in by
 // v_permlane32_swap (VALU, no LDS).  cos/sin rows of the positions a block
@@ -427,23 +432,64 @@ __device__ __forceinline__ void lanes_block(const RopeArgs& a, int hpw, int np_m
   }
 }
 
-// bf16 tables, 16-byte chunks: cos/sin read per item from global (see the
-// header).  IT items per thread, all q/k loads issued first.  With one
-// item a thread also issues its cos/sin (and norm weight) loads before any
-// arithmetic, so a wave waits for memory once; with two, holding both items'
-// tables costs occupancy (84 against 70 VGPRs) and the tables are loaded per
-// item instead.  Measured at q[1,32,3100,128] + k[1,8,...]: plain RoPE 14.5 us
-// with two items (14.9 with one), the norm variant 19.7 us with one (21.3
-// with two), the KV append 15.5 / 20.5 us (plain / norm) with one (17.1 /
-// 22.5 with two).
-template <bool NORM>
-constexpr int direct_items() { return NORM ? 1 : 2; }
+// bf16 tables, 16-byte chunks, read straight from global (see the header):
+// head groups.  A thread owns chunk c of R head rows of one kind (q, k; v for
+// the cache append) at one position -- the chunk pair [8c, 8c + 8) and
+// [D/2 + 8c, +8) of each row -- so the position's cos/sin chunks (and norm
+// weights) are loaded once for R rows instead of once per row.  All of a
+// thread's loads (2R activation chunks, 4 table chunks, 2 weight chunks) are
+// issued before any arithmetic, so a wave waits for memory once.
+// Consecutive threads walk the chunks, then the head groups (q first), then
+// the positions: the chunk lanes of one head row are adjacent and start at a
+// multiple of D/16 (the head-row norm's reduction), and at D = 128 one load
+// instruction covers whole 128-byte half rows.  R is the largest of 4, 2, 1
+// that divides every head count.  Measured at q[1,32,3100,128] +
+// k[1,8,...] in one process: plain RoPE 13.2-13.6 us at R = 4 against
+// 13.6-14.1 us with one row per thread; with the head-row norm 15.4-16.5
+// against 17.1-18.5 us; R = 8 (112 / 136 VGPRs) 14.1 / 17.1-17.9 us.
+// The KV append keeps one head row per thread (kKvItems): head groups there,
+// for the q rows only or for every kind, measured 16.0-16.4 against
+// 15.3-15.9 us plain and 20.3 against 18.5-19.1 us with the norm.
+constexpr int kMaxGroupRows = 4;
 constexpr int kKvItems = 1;
 
+int group_rows(int64_t Hq, int64_t Hk) {
+  for (int r = kMaxGroupRows; r > 1; r /= 2)
+    if (Hq % r == 0 && Hk % r == 0) return r;
+  return 1;
+}
+
+// Thread -> (batch b, position s in the sequence, head group g, chunk c) for
+// tpp threads per position; the block's first position is found once, each
+// thread's offset from it with small divisions (SmallDiv).
+struct GroupItem {
+  int64_t b, s;
+  int g, c;
+};
+
+__device__ __forceinline__ GroupItem group_item(const SmallDiv& tpp, const SmallDiv& chunks,
+                                                int64_t B, int64_t S) {
+  const int64_t base = (int64_t)blockIdx.x * 256;
+  const int64_t pb = base / tpp.d;
+  const int rb = (int)(base - pb * tpp.d);
+  int j;
+  const int64_t p = pb + div_small(tpp, rb + (int)threadIdx.x, j);
+  GroupItem it;
+  it.b = 0;
+  it.s = p;
+  if (B != 1) {
+    it.b = p / S;
+    it.s = p - it.b * S;
+  }
+  it.g = div_small(chunks, j, it.c);
+  return it;
+}
+
 // HF Qwen3VLTextRMSNorm of one head row ahead of its rotation (the text
-// attention's q_norm / k_norm), in place.  A head row is G = D/16 items, one
-// per lane, on G consecutive lanes that start at a multiple of G (rows start
-// at multiples of G items and a block's items are lane-ordered): lane c holds
+// attention's q_norm / k_norm), in place.  A head row is spread over G = D/16
+// consecutive lanes that start at a multiple of G (a row's chunks are
+// consecutive threads, and every position's thread count is a multiple of
+// G): lane c holds
 // the chunks [8c, 8c + 8) (xl) and [D/2 + 8c, +8) (xh); w holds the matching
 // weight chunks.  Called with the whole row active (rows are skipped or kept
 // as a unit).  The statistic follows torch-ROCm's reduction for
@@ -509,98 +555,59 @@ __device__ __forceinline__ void load_item_tables(ItemTables& t, const void* cos,
   }
 }
 
-// The body of rope_qk_direct_kernel for one block; FULL: every item of the
-// block is in range (all blocks but the last), so the per-item guards --
-// branches between the loads and their use -- are compile-time true.
-template <int MODE, bool NORM, bool FULL>
-__device__ __forceinline__ void direct_block(const RopeArgs& a) {
-  constexpr int VEC = 8;
-  constexpr int IT = direct_items<NORM>();
-  const int64_t npos = a.B * a.S;
-  const int D = (int)a.D;
-  const int half = D / 2;
-  const int ipp = a.ipp.d;
-  const int nq = (int)a.Hq * a.chunks.d;
-  const int64_t nitems = npos * ipp;
-  // block-level decomposition once, per item small divisions (SmallDiv)
-  const int64_t base = (int64_t)blockIdx.x * (IT * 256);
-  const int64_t pb = base / ipp;
-  const int rb = (int)(base - pb * ipp);
-  const uint16_t* xs[IT];
-  uint16_t* os[IT];
-  int64_t cso[IT];
-  int dls[IT];
-  bool ok[IT], qrow[IT];
-#pragma unroll
-  for (int u = 0; u < IT; ++u) {
-    const int l = u * 256 + (int)threadIdx.x;
-    ok[u] = FULL || base + l < nitems;
-    int j;
-    const int pp = div_small(a.ipp, rb + l, j);
-    int64_t p = pb + pp;
-    if (!FULL && !ok[u]) p = 0, j = 0;  // re-reads item 0 (always valid) and stores nothing
-    int64_t b = 0, sidx = p;
-    if (a.B != 1) {
-      b = p / a.S;
-      sidx = p - b * a.S;
-    }
-    const bool isq = j < nq;
-    qrow[u] = isq;
-    const int jj = isq ? j : j - nq;
-    int c;
-    const int h = div_small(a.chunks, jj, c);
-    if (isq) {
-      xs[u] = a.q + b * a.q_sb + sidx * a.q_ss + h * a.q_sh;
-      os[u] = a.qo + b * a.qo_sb + sidx * a.qo_ss + h * a.qo_sh;
-    } else {
-      xs[u] = a.k + b * a.k_sb + sidx * a.k_ss + h * a.k_sh;
-      os[u] = a.ko + b * a.ko_sb + sidx * a.ko_ss + h * a.ko_sh;
-    }
-    dls[u] = c * VEC;
-    cso[u] = b * a.cs_sb + sidx * a.cs_ss;
+// q / k rotation (after the head-row norm when NORM) of R head rows per
+// thread; a.chunks = D/16, tpp = (Hq/R + Hk/R) * D/16 threads per position,
+// gq = Hq/R q groups, nthreads = B * S * tpp.
+template <int MODE, bool NORM, int R>
+__global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a, SmallDiv tpp, int gq,
+                                                             int64_t nthreads) {
+  // a head row's chunk lanes leave together (nthreads is a multiple of D/16)
+  if ((int64_t)blockIdx.x * 256 + (int64_t)threadIdx.x >= nthreads) return;
+  const GroupItem it = group_item(tpp, a.chunks, a.B, a.S);
+  const bool isq = it.g < gq;
+  const int64_t h0 = (int64_t)(isq ? it.g : it.g - gq) * R;
+  const int half = (int)a.D / 2;
+  const int dl = it.c * 8;
+  const uint16_t* x;
+  uint16_t* o;
+  int64_t xsh, osh;
+  if (isq) {
+    x = a.q + it.b * a.q_sb + it.s * a.q_ss + h0 * a.q_sh + dl;
+    o = a.qo + it.b * a.qo_sb + it.s * a.qo_ss + h0 * a.qo_sh + dl;
+    xsh = a.q_sh;
+    osh = a.qo_sh;
+  } else {
+    x = a.k + it.b * a.k_sb + it.s * a.k_ss + h0 * a.k_sh + dl;
+    o = a.ko + it.b * a.ko_sb + it.s * a.ko_ss + h0 * a.ko_sh + dl;
+    xsh = a.k_sh;
+    osh = a.ko_sh;
   }
   // held packed until use (8 registers per half chunk instead of 16)
-  u32x4 rl[IT], rh[IT];
-  ItemTables tb[IT];
+  u32x4 rl[R], rh[R];
 #pragma unroll
-  for (int u = 0; u < IT; ++u) {
-    rl[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + dls[u]));
-    rh[u] = ld_stream(reinterpret_cast<const u32x4*>(xs[u] + half + dls[u]));
+  for (int r = 0; r < R; ++r) {
+    rl[r] = ld_stream(reinterpret_cast<const u32x4*>(x + r * xsh));
+    rh[r] = ld_stream(reinterpret_cast<const u32x4*>(x + r * xsh + half));
   }
-  if constexpr (IT == 1)
-    load_item_tables<NORM>(tb[0], a.cos, a.sin, cso[0], dls[0], half, qrow[0] ? a.qw : a.kw);
+  ItemTables tb;
+  load_item_tables<NORM>(tb, a.cos, a.sin, it.b * a.cs_sb + it.s * a.cs_ss, dl, half,
+                         isq ? a.qw : a.kw);
+  float cl[8], ch[8], sl[8], sh[8];
+  unpack8(tb.cs[0], cl);
+  unpack8(tb.cs[1], ch);
+  unpack8(tb.cs[2], sl);
+  unpack8(tb.cs[3], sh);
 #pragma unroll
-  for (int u = 0; u < IT; ++u) {
-    if (!FULL && !ok[u]) continue;
-    if constexpr (IT > 1)
-      load_item_tables<NORM>(tb[u], a.cos, a.sin, cso[u], dls[u], half, qrow[u] ? a.qw : a.kw);
-    float xl[VEC], xh[VEC];
-    unpack8(rl[u], xl);
-    unpack8(rh[u], xh);
+  for (int r = 0; r < R; ++r) {
+    float xl[8], xh[8], ol[8], oh[8];
+    unpack8(rl[r], xl);
+    unpack8(rh[r], xh);
     if constexpr (NORM)
-      rms_norm_chunks(xl, xh, tb[u].w, a.chunks.d, qrow[u] ? a.fq : a.fk, a.eps);
-    float cl[VEC], ch[VEC], sl[VEC], sh[VEC], ol[VEC], oh[VEC];
-    unpack8(tb[u].cs[0], cl);
-    unpack8(tb[u].cs[1], ch);
-    unpack8(tb[u].cs[2], sl);
-    unpack8(tb[u].cs[3], sh);
-    rotate<MODE, VEC>(xl, xh, cl, ch, sl, sh, ol, oh);
-    Chunk<VEC>::store(os[u] + dls[u], ol);
-    Chunk<VEC>::store(os[u] + half + dls[u], oh);
+      rms_norm_chunks(xl, xh, tb.w, a.chunks.d, isq ? a.fq : a.fk, a.eps);
+    rotate<MODE, 8>(xl, xh, cl, ch, sl, sh, ol, oh);
+    Chunk<8>::store(o + r * osh, ol);
+    Chunk<8>::store(o + r * osh + half, oh);
   }
-}
-
-// Plain RoPE (two items per thread) takes the guard-free body in full blocks:
-// 13.6-14.7 against 14.2-14.7 us at q[1,32,3100,128]; with the head-row norm
-// (one item) it measured no better, so that form keeps the single body.
-template <int MODE, bool NORM = false>
-__global__ __launch_bounds__(256) void rope_qk_direct_kernel(RopeArgs a) {
-  constexpr int IT = direct_items<NORM>();
-  const int64_t nitems = a.B * a.S * a.ipp.d;
-  if (IT > 1 && (int64_t)(blockIdx.x + 1) * (IT * 256) <= nitems)
-    direct_block<MODE, NORM, IT != 1>(a);
-  else
-    direct_block<MODE, NORM, false>(a);
 }
 
 // Text RoPE fused with the append into an in-place KV cache.  Per position
@@ -792,9 +799,31 @@ int launch_staged(const RopeArgs& a0, hipStream_t st) {
   return launch_status();
 }
 
+// The head-group kernel for R rows per thread; a carries its divisors.
+template <int MODE, bool NORM, int R>
+int launch_direct_r(const RopeArgs& a, hipStream_t st) {
+  const int gq = (int)(a.Hq / R), gk = (int)(a.Hk / R);
+  const SmallDiv tpp = small_div((gq + gk) * a.chunks.d);
+  const int64_t nthreads = a.B * a.S * tpp.d;
+  const int64_t blocks = (nthreads + 255) / 256;
+  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((rope_qk_direct_kernel<MODE, NORM, R>), dim3((unsigned)blocks), dim3(256),
+                     0, st, a, tpp, gq, nthreads);
+  return launch_status();
+}
+
+template <int MODE, bool NORM>
+int launch_direct(const RopeArgs& a, hipStream_t st) {
+  switch (group_rows(a.Hq, a.Hk)) {
+    case 4: return launch_direct_r<MODE, NORM, 4>(a, st);
+    case 2: return launch_direct_r<MODE, NORM, 2>(a, st);
+    default: return launch_direct_r<MODE, NORM, 1>(a, st);
+  }
+}
+
 // direct_ok: the bf16 tables allow 16-byte reads (aligned bases, row
 // strides multiples of 8 elements); otherwise they are staged.  The
-// item-pair forms are kept for head dims whose half rows are whole 128-byte
+// head-group and item-pair forms are kept for head dims whose half rows are whole 128-byte
 // lines (D a multiple of 128); any other D with 16-byte chunks takes the
 // lane-chunk form (at D = 80 with bf16 tables 33-37 against 38-41 us, at
 // text D = 64 9.5 against 14.4-15.3 us).
@@ -808,13 +837,7 @@ int launch_rope(const RopeArgs& a, bool direct_ok, hipStream_t st) {
   }
   if constexpr (!CS32 && VEC == 8) {
     if (!direct_ok) return launch_staged<MODE, CS32, VEC>(a, st);
-    const int64_t nitems = a.B * a.S * (a.Hq + a.Hk) * (a.D / 2 / VEC);
-    constexpr int per_block = direct_items<false>() * 256;
-    const int64_t blocks = (nitems + per_block - 1) / per_block;
-    if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((rope_qk_direct_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       with_divisors<VEC>(a));
-    return launch_status();
+    return launch_direct<MODE, false>(with_divisors<VEC>(a), st);
   } else {
     return launch_staged<MODE, CS32, VEC>(a, st);
   }
@@ -1029,11 +1052,5 @@ extern "C" int umic_qk_rmsnorm_rope_bf16(const void* q, const void* k, void* q_o
   a.eps = eps;
   a.fq = mean_factor(B * S * Hq, D);
   a.fk = mean_factor(B * S * Hk, D);
-  const int64_t nitems = B * S * (Hq + Hk) * (D / 16);
-  constexpr int per_block = direct_items<true>() * 256;
-  const int64_t blocks = (nitems + per_block - 1) / per_block;
-  if (blocks > 0x7fffffffLL) return UMIC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((rope_qk_direct_kernel<UMIC_ROPE_TEXT, true>), dim3((unsigned)blocks),
-                     dim3(256), 0, as_stream(stream), a);
-  return launch_status();
+  return launch_direct<UMIC_ROPE_TEXT, true>(a, as_stream(stream));
 }
