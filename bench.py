@@ -31,7 +31,10 @@ time.  ms_per_step is the sum over kernels of the per-launch event time.
 Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
 six fused norm/RoPE kernels (algorithmic bytes / summed durations);
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
-(by time) of the step; cpu_baseline = the reference's own CPU path (HF's
+(by time) of the step, its traffic (HBM bytes per launch) measured after the
+timed region by two rocprofv3 --pmc child runs of --pmc-probe (FETCH_SIZE,
+WRITE_SIZE, scaled by a device copy of known size; the committed PMC summary
+when the profiler is absent or --no-traffic is given); cpu_baseline = the reference's own CPU path (HF's
 eager Qwen3-VL modules, RoPE functions and the eager P5 chain in torch, bf16,
 on the host cores) over all five BASELINE configs at full size, value in GB/s
 over the norm/RoPE ops as for the GPU; cpu_oracle = the scalar C oracle (one
@@ -444,8 +447,63 @@ def load_traffic(name: str):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def pmc_probe() -> int:
-    """One launch of each kernel after a plain device copy of known size.
+# kernel-name fragment of each bench entry whose traffic can be measured live
+TRAFFIC_KERNELS = {"gate_silu_mul": "gemm_kernel<2,", "q_proj/o_proj": "gemm_kernel<1,",
+                   "down_proj": "gemm_sk_kernel<"}
+COPY_KERNEL = "__amd_rocclr_copyBuffer"  # the HIP runtime's device copy (the probe's calibration)
+
+
+def measure_traffic(name: str):
+    """HBM bytes per launch of bench entry `name`, measured in this run.
+
+    Two child runs of ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) over
+    this script's ``--pmc-probe`` mode, restricted to the calibration copy and
+    that kernel (one launch each, after a 1 GiB fill that evicts the Infinity
+    Cache).  Each counter is scaled by what it reads for the copy, which moves
+    exactly COPY_BYTES each way.  Returns (bytes, scales, None) or
+    (None, None, reason) when the profiler is absent or a pass fails.
+    """
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    frag = TRAFFIC_KERNELS.get(name)
+    prof = shutil.which("rocprofv3")
+    if frag is None or prof is None:
+        return None, None, "no live measurement for this kernel" if prof else "rocprofv3 not found"
+    env = dict(os.environ, TMPDIR="/tmp")
+    vals = {}
+    with tempfile.TemporaryDirectory(prefix="umic_pmc_", dir="/tmp") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            out = os.path.join(tmp, counter)
+            cmd = ["timeout", "-s", "KILL", "150", prof, "--pmc", counter, "-d", out, "-o",
+                   "probe", "--output-format", "csv", "--", sys.executable, "-u",
+                   os.path.abspath(__file__), "--pmc-probe", "--probe-only", name]
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+            if r.returncode != 0:
+                return None, None, f"{counter} pass exited with {r.returncode}"
+            files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                return None, None, f"{counter} pass wrote no counter file"
+            with open(files[0]) as f:
+                rows = list(csv.DictReader(f))
+            copy = [float(x["Counter_Value"]) for x in rows if COPY_KERNEL in x["Kernel_Name"]]
+            kern = [float(x["Counter_Value"]) for x in rows if frag in x["Kernel_Name"]]
+            if not copy or not kern or copy[-1] <= 0:
+                return None, None, f"{counter} pass: calibration copy or kernel not found"
+            vals[counter] = (copy[-1], kern[-1])
+    true_kb = COPY_BYTES / 1024
+    rs, ws = true_kb / vals["FETCH_SIZE"][0], true_kb / vals["WRITE_SIZE"][0]
+    nbytes = (vals["FETCH_SIZE"][1] * rs + vals["WRITE_SIZE"][1] * ws) * 1024
+    return int(nbytes), {"fetch_kb": vals["FETCH_SIZE"][1], "write_kb": vals["WRITE_SIZE"][1],
+                         "read_scale": round(rs, 4), "write_scale": round(ws, 4)}, None
+
+
+def pmc_probe(only=None) -> int:
+    """One launch of each kernel (or of the entries named in ``only``) after a
+    plain device copy of known size.
 
     Run under ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``): the copy
     reads and writes exactly COPY_BYTES, which calibrates the counters'
@@ -472,8 +530,10 @@ def pmc_probe() -> int:
           2 * 2 * 48 * S * D + 2 * 2 * S * D)
     torch.cuda.synchronize()
     # one kernel per probe: the unfused comparison (three launches) is left out
-    single = [e for e in ents if not e[0].endswith("_unfused")]
-    for name, fn, nbytes, *_ in [("copy", lambda i: dst.copy_(src), 2 * COPY_BYTES)] + single + [kv]:
+    single = [e for e in ents if not e[0].endswith("_unfused")] + [kv]
+    if only:
+        single = [e for e in single if e[0] in only]
+    for name, fn, nbytes, *_ in [("copy", lambda i: dst.copy_(src), 2 * COPY_BYTES)] + single:
         flush.zero_()  # evict the Infinity Cache between probes
         torch.cuda.synchronize()
         fn(0)
@@ -841,6 +901,13 @@ def main() -> int:
                     help="print only the CPU baselines (no GPU needed)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="one launch per kernel after a calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--probe-only", default=None,
+                    help="with --pmc-probe: comma-separated bench entries to launch "
+                         "(after the calibration copy)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="take roofline.traffic from the committed PMC summary instead of "
+                         "measuring it (two rocprofv3 --pmc child runs); use when this run "
+                         "is itself under rocprofv3")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain device copies of the norm/RoPE byte counts")
     ap.add_argument("--vit-sites", action="store_true",
@@ -865,7 +932,7 @@ def main() -> int:
                           "cpu_oracle": cpu_oracle(args.cpu_sample_s)}), flush=True)
         return 0
     if args.pmc_probe:
-        return pmc_probe()
+        return pmc_probe(args.probe_only.split(",") if args.probe_only else None)
     if args.copy_ceiling:
         return copy_ceiling()
     if args.vit_sites:
@@ -928,7 +995,19 @@ def main() -> int:
     else:
         roof = {"kernel": dom_name, "bound": "mfma", "achieved": dom["tflops"],
                 "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"]}
-    roof["traffic"] = load_traffic(dom_name)
+    traffic, scales, why = (None, None, "--no-traffic") if args.no_traffic else \
+        measure_traffic(dom_name)
+    if traffic is not None:
+        roof["traffic"] = traffic
+        roof["traffic_source"] = ("measured in this run: rocprofv3 --pmc FETCH_SIZE, then "
+                                  "WRITE_SIZE, over bench.py --pmc-probe --probe-only "
+                                  f"{dom_name}; counters scaled by a {COPY_BYTES >> 20} MiB "
+                                  "device copy")
+        roof["traffic_counters"] = scales
+    else:
+        roof["traffic"] = load_traffic(dom_name)
+        roof["traffic_source"] = (f"committed profiles/traffic_{dom_name}.json (not measured "
+                                  f"in this run: {why})")
     roof["algorithmic_bytes"] = dom["bytes"]
 
     out = {
