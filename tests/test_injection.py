@@ -404,6 +404,11 @@ def test_apply_report():
     report3 = optimize.apply(_wrap(lm=tiny_text_model()),
                              optimize.UmicConfig(decode_graph=False, adaptive_flow=True))
     assert report3["decode_cache_hook"] is True and report3["adaptive_flow"] is False
+    # the expert's fusions follow flow_cache (the reference nests them under it)
+    report4 = optimize.apply(_wrap(lm=tiny_text_model(), expert=tiny_text_model(layers=1)),
+                             optimize.UmicConfig(flow_cache=False))
+    assert not [k for k in report4 if k.startswith(("expert_", "flow_cache"))]
+    assert report4["lm_rmsnorm_fused"] == 9
     integrate.unfuse_rope()
 
 
