@@ -70,11 +70,15 @@ def test_text_rope_hf_layout(S, Hq, Hk, D):
     assert torch.equal(qo, rq) and torch.equal(ko, rk)
 
 
-def test_text_rope_contiguous_and_batched():
+@pytest.mark.parametrize("Hq,Hk", [(8, 2), (8, 4), (6, 3)])
+def test_text_rope_contiguous_and_batched(Hq, Hk):
+    """Contiguous [B, H, S, D] q/k (head strides S * D) with two head rows
+    per thread (8 / 2), four (8 / 4) and one (6 / 3), per-batch and
+    batch-broadcast tables."""
     from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb
 
     g = torch.Generator().manual_seed(1)
-    B, S, Hq, Hk, D = 2, 100, 8, 2, 128
+    B, S, D = 2, 100, 128
     cos, sin = text_tables(S, D, 1e6, B=B, offsets=(0, 500))
     q = bf16_randn(B, Hq, S, D, gen=g).to(DEV)          # contiguous [B,H,S,D]
     k = bf16_randn(B, Hk, S, D, gen=g).to(DEV)
@@ -149,6 +153,30 @@ def test_vision_rope_bf16_tables_and_fallback_wrapper():
     fused = rope.make_vision_rope(apply_rotary_pos_emb_vision)
     qo, ko = fused(q, k, cos, sin)
     rq, rk = apply_rotary_pos_emb_vision(q, k, cos, sin)
+    assert torch.equal(qo, rq) and torch.equal(ko, rk)
+
+
+@pytest.mark.parametrize("S,H,D", [(300, 4, 128), (77, 6, 128), (19, 3, 256), (1, 4, 256)])
+def test_vision_rope_bf16_tables_head_groups(S, H, D):
+    """bf16 tables and head dims that are whole 128-byte half rows take the
+    head-group kernel in its vision arithmetic (fp32 ops, one rounding): four
+    (H = 4), two (6) or one (3) head rows per thread.  Bit for bit with the
+    oracle on the exactly widened tables and with HF on the GPU."""
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import apply_rotary_pos_emb_vision
+
+    print(f"vision head groups S={S} H={H} D={D}", flush=True)
+    g = torch.Generator().manual_seed(S * 7 + D + H)
+    qkv = bf16_randn(S, 3, H, D, gen=g)
+    ang = 3.0 * torch.randn(S, D, generator=g)
+    c, s_ = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    q, k, _ = qkv.to(DEV).permute(1, 0, 2, 3).unbind(0)
+    qo, ko = rope.apply_rotary_vision_hip(q, k, c.to(DEV), s_.to(DEV))
+    torch.cuda.synchronize()
+    qc, kc, _ = qkv.permute(1, 0, 2, 3).unbind(0)
+    cn, sn = c.float().numpy(), s_.float().numpy()
+    assert np.array_equal(bits(qo), oracle.rope_vision(bits(qc), cn, sn))
+    assert np.array_equal(bits(ko), oracle.rope_vision(bits(kc), cn, sn))
+    rq, rk = apply_rotary_pos_emb_vision(q, k, c.to(DEV), s_.to(DEV))
     assert torch.equal(qo, rq) and torch.equal(ko, rk)
 
 
