@@ -488,17 +488,36 @@ def measure_traffic(name: str):
             if not files:
                 return None, None, f"{counter} pass wrote no counter file"
             with open(files[0]) as f:
-                rows = list(csv.DictReader(f))
-            copy = [float(x["Counter_Value"]) for x in rows if COPY_KERNEL in x["Kernel_Name"]]
-            kern = [float(x["Counter_Value"]) for x in rows if frag in x["Kernel_Name"]]
-            if not copy or not kern or copy[-1] <= 0:
+                vals[counter] = pmc_copy_and_kernel(csv.DictReader(f), frag)
+            if vals[counter] is None:
                 return None, None, f"{counter} pass: calibration copy or kernel not found"
-            vals[counter] = (copy[-1], kern[-1])
+    return (*calibrated_traffic(vals["FETCH_SIZE"], vals["WRITE_SIZE"]), None)
+
+
+def pmc_copy_and_kernel(rows, frag: str):
+    """(calibration copy's counter value, kernel's value) from rocprofv3
+    counter-collection rows (one row per dispatch), the last dispatch of
+    each; None if either is missing or the copy read zero."""
+    copy, kern = [], []
+    for r in rows:
+        if COPY_KERNEL in r["Kernel_Name"]:
+            copy.append(float(r["Counter_Value"]))
+        elif frag in r["Kernel_Name"]:
+            kern.append(float(r["Counter_Value"]))
+    if not copy or not kern or copy[-1] <= 0:
+        return None
+    return copy[-1], kern[-1]
+
+
+def calibrated_traffic(fetch, write):
+    """HBM bytes of the kernel from (copy KB, kernel KB) of FETCH_SIZE and of
+    WRITE_SIZE: each counter scaled by COPY_BYTES over what it read for the
+    copy, which moves exactly COPY_BYTES each way."""
     true_kb = COPY_BYTES / 1024
-    rs, ws = true_kb / vals["FETCH_SIZE"][0], true_kb / vals["WRITE_SIZE"][0]
-    nbytes = (vals["FETCH_SIZE"][1] * rs + vals["WRITE_SIZE"][1] * ws) * 1024
-    return int(nbytes), {"fetch_kb": vals["FETCH_SIZE"][1], "write_kb": vals["WRITE_SIZE"][1],
-                         "read_scale": round(rs, 4), "write_scale": round(ws, 4)}, None
+    rs, ws = true_kb / fetch[0], true_kb / write[0]
+    nbytes = (fetch[1] * rs + write[1] * ws) * 1024
+    return int(nbytes), {"fetch_kb": fetch[1], "write_kb": write[1],
+                         "read_scale": round(rs, 4), "write_scale": round(ws, 4)}
 
 
 def pmc_probe(only=None) -> int:
