@@ -478,7 +478,9 @@ def measure_traffic(name: str):
     with tempfile.TemporaryDirectory(prefix="umic_pmc_", dir="/tmp") as tmp:
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             out = os.path.join(tmp, counter)
-            cmd = ["timeout", "-s", "KILL", "150", prof, "--pmc", counter, "-d", out, "-o",
+            # a pass takes a few seconds; the kill bound keeps a stuck profiler
+            # from holding the run
+            cmd = ["timeout", "-s", "KILL", "90", prof, "--pmc", counter, "-d", out, "-o",
                    "probe", "--output-format", "csv", "--", sys.executable, "-u",
                    os.path.abspath(__file__), "--pmc-probe", "--probe-only", name]
             r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
