@@ -396,6 +396,13 @@ def test_apply_report():
     assert report["lm_kv_rope_fused"] == 2 and report["expert_kv_rope_fused"] == 1
     assert report["flow_cache_hook"] is True and report["decode_graph"] is True
     assert "decode_cache_hook" not in report and "adaptive_flow" not in report
+    # application order: the reference's (LM, text RoPE, ViT, expert, VLM), with
+    # this runtime's additions next to the fusion each extends
+    assert list(report) == [
+        "lm_mlp_fused", "lm_linear_fused", "lm_rmsnorm_fused", "lm_add_rmsnorm_fused",
+        "text_rope_fused", "lm_kv_rope_fused", "ve_layernorm_fused", "ve_rope_fused",
+        "ve_pipeline_fused", "ve_gelu_mlp_fused", "flow_cache_hook", "expert_rmsnorm_fused",
+        "expert_add_rmsnorm_fused", "expert_kv_rope_fused", "decode_graph"]
     cfg = optimize.UmicConfig(mlp_fusion=False, vision_fusion=False, decode_graph=False,
                               flow_cache=False, decode_cache=False)
     report2 = optimize.apply(_wrap(lm=tiny_text_model()), cfg)
