@@ -1006,9 +1006,8 @@ int launch_gemm_sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
   g.tiles_m = (int)((g.M + kBM - 1) / kBM);
   g.tiles = (int)pl.tiles;
   g.bm = kBM;
-  // whole tile columns: the CUs that split a column's K range share its
-  // weight slab (down_proj at M = 3100: 269.6-272.4 against 284.1-286.3 us
-  // with groups of four rows, one process)
+  // whole tile columns, m fastest: down_proj at M = 3100 ran 266-269 us
+  // against 280-282 us with groups of four tile rows (one process)
   g.gm = g.tiles_m;
   SkArgs s{static_cast<int*>(ws),
            reinterpret_cast<f32x4_t*>(static_cast<char*>(ws) + pl.counter_bytes), (int)pl.tiles,
