@@ -54,10 +54,10 @@ def _capture(fn: Callable[[], Any], pool=None, warm: bool = True):
     Python's cyclic garbage collector is held off while the capture is open.
     A collection there finalizes whatever dead cycles exist at that moment --
     a discarded runner is one (the model's forward holds the runner, which
-    holds the model) -- and so destroys their graphs and releases their graph
-    memory pools inside another stream capture, which HIP does not allow (the
-    process aborted that way).  torch.cuda.graph no longer collects before a
-    capture by default, so the guard is here."""
+    holds the model) -- and so can destroy their graphs and release their
+    graph memory pools inside another stream capture; a test process once
+    aborted during such a collection.  torch.cuda.graph no longer collects
+    before a capture by default, so the guard is here."""
     if warm:
         _on_side_stream(fn)
     graph = torch.cuda.CUDAGraph()
