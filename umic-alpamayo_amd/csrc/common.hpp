@@ -140,9 +140,30 @@ __device__ __forceinline__ double group_sum(double v) { return group_sum_dpp<G>(
 template <int G>
 __device__ __forceinline__ float group_sum(float v) { return group_sum_dpp<G>(v); }
 
-// Correctly rounded fp32 1/sqrt(v): evaluated in double, rounded once.
+// Correctly rounded fp32 1/sqrt(v).  For a positive normal v the hardware
+// estimate y = v_rsq_f32(v) is within an ulp, so the result is y or a
+// neighbour, and the midpoint m between y and a neighbour decides:
+// 1/sqrt(v) > m exactly when v * m^2 < 1, and fma(v, m * m, -1) in double has
+// that sign exactly (m has at most 25 significant bits, so m * m is exact, and
+// the fma rounds once).  1/sqrt(v) never equals a midpoint (v would be 1/m^2,
+// not a float).  Inputs below the normal range are scaled by 2^64 and the
+// result by 2^32 (both exact); zero, infinities, NaN and negatives come out of
+// the estimate unchanged.  Selects, no branches: a branch here sat between a
+// row's stores and cost add+RMSNorm 4%.  Checked on MI355X against
+// (float)(1.0 / sqrt((double)v)) for every non-negative finite float and the
+// special values: identical, at about a third of that quotient's fp64 work.
 __device__ __forceinline__ float rsqrt_cr(float v) {
-  return (float)(1.0 / __builtin_sqrt((double)v));
+  const bool tiny = v < 0x1p-126f;
+  const float vs = tiny ? v * 0x1p64f : v;
+  const float y = __builtin_amdgcn_rsqf(vs);
+  const uint32_t yb = __float_as_uint(y);
+  const float up = __uint_as_float(yb + 1u), dn = __uint_as_float(yb - 1u);
+  const double vd = vs, yd = y;
+  const double mu = 0.5 * (yd + (double)up), md = 0.5 * (yd + (double)dn);
+  const bool go_up = __builtin_fma(vd, mu * mu, -1.0) < 0.0;
+  const bool go_dn = __builtin_fma(vd, md * md, -1.0) > 0.0;
+  const float r = go_up ? up : go_dn ? dn : y;
+  return tiny ? r * 0x1p32f : r;
 }
 
 // ---- host-side argument checks -------------------------------------------
