@@ -46,6 +46,14 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 // fp32 value of bf16(f)
 __device__ __forceinline__ float rbf(float f) { return (float)(__bf16)f; }
 
+// rbf of two values through one paired conversion (v_cvt_pk_bf16_f32 and two
+// extractions: three VALU instructions where two rbf take four)
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+  const uint32_t w = pack2(a, b);
+  a = bf_lo(w);
+  b = bf_hi(w);
+}
+
 // 8 bf16 values <-> 8 floats
 __device__ __forceinline__ void unpack8(const u32x4& v, float f[8]) {
   f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
