@@ -267,7 +267,12 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int
       unpack8(sv[r][i], f);
       unpack8(wv[i], wf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+      for (int e = 0; e < 8; e += 2) {  // bf16(x * rstd) in pairs (one conversion each)
+        float p0 = f[e] * rstd, p1 = f[e + 1] * rstd;
+        rbf2(p0, p1);
+        o[e] = wf[e] * p0;
+        o[e + 1] = wf[e + 1] * p1;
+      }
       st_stream(yp + cix[i], pack8(o));
     }
   }
@@ -588,7 +593,12 @@ __global__ __launch_bounds__(BW) void rms_wide_kernel(NormArgs a) {
     unpack4(v[k], f);
     unpack4(*reinterpret_cast<const u32x2*>(wr + idx * 4), wf);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = wf[e] * rbf(f[e] * rstd);
+    for (int e = 0; e < 4; e += 2) {  // bf16(x * rstd) in pairs
+      float p0 = f[e] * rstd, p1 = f[e + 1] * rstd;
+      rbf2(p0, p1);
+      o[e] = wf[e] * p0;
+      o[e + 1] = wf[e + 1] * p1;
+    }
     *reinterpret_cast<u32x2*>(yr + idx * 4) = pack4(o);
   }
 }
