@@ -446,8 +446,9 @@ __device__ __forceinline__ void lanes_block(const RopeArgs& a, int hpw, int np_m
 // the cache append) at one position -- the chunk pair [8c, 8c + 8) and
 // [D/2 + 8c, +8) of each row -- so the position's cos/sin chunks (and norm
 // weights) are loaded once for R rows instead of once per row.  All of a
-// thread's loads (2R activation chunks, 4 table chunks, 2 weight chunks) are
-// issued before any arithmetic, so a wave waits for memory once.
+// thread's loads (4 table chunks, 2 weight chunks, then 2R activation chunks)
+// are issued before any arithmetic; row r's arithmetic waits only for the
+// tables and its own chunks.
 // Consecutive threads walk the chunks, then the head groups (q first), then
 // the positions: the chunk lanes of one head row are adjacent and start at a
 // multiple of D/16 (the head-row norm's reduction), and at D = 128 one load
@@ -548,8 +549,7 @@ __device__ __forceinline__ u32x4 ld_chunk(const void* base, int64_t off) {
 }
 
 // The cos/sin chunks of an item (low and high half of each table) and, for
-// the norm kernels, its row's weight chunks -- all loads of a thread are
-// issued before any item is computed, so a wave waits for memory once.
+// the norm kernels, its row's weight chunks.
 struct ItemTables {
   u32x4 cs[4];  // cos lo, cos hi, sin lo, sin hi
   u32x4 w[2];   // norm weight lo, hi
