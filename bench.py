@@ -29,7 +29,10 @@ before the first event fires and host launch latency never shows up as GPU
 time.  ms_per_step is the sum over kernels of the per-launch event time.
 
 Output: one JSON line (rank 0).  value = aggregate achieved HBM GB/s of the
-six fused norm/RoPE kernels (algorithmic bytes / summed durations);
+six fused norm/RoPE kernels (algorithmic bytes / summed durations); each
+HBM-bound kernel also carries the time of a plain device copy of its byte
+count (copy_us, of_copy = copy time / kernel time), and copy_ceiling_gbps /
+of_copy give the same for the six together;
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
 (by time) of the step, its traffic (HBM bytes per launch) measured at the
 end of the run, after every timed step, by two rocprofv3 --pmc child runs of --pmc-probe (FETCH_SIZE,
@@ -594,6 +597,30 @@ def copy_ceiling() -> int:
     return 0
 
 
+def same_bytes_copy(moved: int, steps: int) -> float:
+    """Event-timed microseconds of one device copy (torch copy_, the HIP
+    runtime's blit kernel) that reads moved/2 and writes moved/2 bytes: the
+    practical ceiling of an HBM-bound kernel moving the same bytes.  The
+    pairs rotate like the kernels' input rings (a pair returns only after
+    >= 640 MB of other traffic), so the Infinity Cache serves none of it."""
+    import torch
+
+    n = moved // 4  # bf16 elements per side
+    pairs = max(2, min(16, int(-(-640e6 // moved))))
+    src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(pairs)]
+    dst = [torch.empty_like(src[0]) for _ in range(pairs)]
+    for i in range(pairs):
+        dst[i].copy_(src[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        dst[i % pairs].copy_(src[i % pairs])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
 def _config5_layer():
     """BASELINE config 5 text decoder layer in bf16 on the GPU with random
     N(0, 0.02) weights (norms 1 + N(0, 0.1)), its rotary embedding and the
@@ -1012,6 +1039,19 @@ def main() -> int:
             rec["frac"] = round(rec["tflops"] / BF16_PEAK_TFLOPS, 4)
         kern[name] = rec
 
+    # each HBM-bound kernel against a plain device copy of its byte count,
+    # timed the same way right after the kernels: of_copy = copy time / kernel
+    # time (1.0 = as fast as the runtime's own copy of those bytes)
+    copy_us = {}
+    for name, rec in kern.items():
+        if rec["bound"] == "hbm":
+            if rec["bytes"] not in copy_us:
+                copy_us[rec["bytes"]] = same_bytes_copy(rec["bytes"], K)
+            c = copy_us[rec["bytes"]]
+            rec["copy_us"] = round(c, 2)
+            rec["copy_gbps"] = round(rec["bytes"] / (c * 1e-6) / 1e9, 1)
+            rec["of_copy"] = round(c / rec["us"], 3)
+
     hbm = [kern[n] for n in VALUE_SITES]
     agg = sum(k["bytes"] for k in hbm) / (sum(k["us"] for k in hbm) * 1e-6) / 1e9
     mlp_ms = (kern["gate_silu_mul"]["us"] + kern["down_proj"]["us"]) / 1e3
@@ -1067,6 +1107,12 @@ def main() -> int:
                                "down_proj K=12288 N=4096",
                    "rows_lm": 3100, "rows_vit": 16384, "input_rings": rings},
         "hbm_frac": round(agg / HBM_PEAK_GBS, 4),
+        # the same six kernels against same-size device copies (kernels[..]
+        # .copy_us): aggregate copy GB/s over those byte counts, and the
+        # kernels' aggregate as a fraction of it
+        "copy_ceiling_gbps": round(sum(k["bytes"] for k in hbm)
+                                   / (sum(k["copy_us"] for k in hbm) * 1e-6) / 1e9, 1),
+        "of_copy": round(sum(k["copy_us"] for k in hbm) / sum(k["us"] for k in hbm), 3),
         "mlp_prefill_ms": round(mlp_ms, 4),
         "kernels": kern,
         "roofline": roof,

@@ -36,6 +36,16 @@ extern "C" {
 #define UMIC_ERR_UNSUPPORTED (-2)  /* shape / stride / alignment not handled */
 #define UMIC_ERR_SCRATCH (-3)      /* shape needs more than the static scratch */
 
+/* Byte offset, in a stream-K workspace, of its sticky status word (int32):
+ * 0 while every split tile's reduction has completed; 1 + t after the last
+ * workgroup to reach tile t gave up waiting for the tile's other segments
+ * (a bounded wait of well under a second: the workspace's counters were
+ * inconsistent, e.g. calls overlapping on one workspace).  Tile t's output
+ * is then left unwritten and its counters reset; the launch ends normally.
+ * No launch clears the word: the caller reads it (and clears it) when it
+ * wants to know. */
+#define UMIC_SK_STATUS_OFFSET 8192
+
 /* Library version string, e.g. "umic-hip 0.1.0 gfx950". */
 const char* umic_version(void);
 
@@ -244,8 +254,11 @@ int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * aligned, ALL ZERO before its first use; every call leaves its counters at
  * zero again, so one workspace serves any number of calls that do not
  * overlap in time (e.g. all calls on one stream).  Calls that may run
- * concurrently need separate workspaces.  A smaller (or NULL) workspace, or
- * a shape the data-parallel kernel serves better, runs umic_linear_bf16.
+ * concurrently need separate workspaces: overlapping calls on one workspace
+ * may give wrong results, or make a tile's reduction wait give up (see
+ * UMIC_SK_STATUS_OFFSET), leaving that tile unwritten.  A smaller (or NULL)
+ * workspace, or a shape the data-parallel kernel serves better, runs
+ * umic_linear_bf16.
  * Replaces: kernels/linear.py:118-145 (linear_triton), as umic_linear_bf16;
  * caller integrate.py:98-107.
  */
@@ -263,11 +276,16 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
  * enough workspace; shapes the data-parallel kernel or the GEMV serve run
  * those, as there.  A shape whose stream-K workspace
  * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 85 output tiles
- * of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  Each call
- * clears the scratch's tile counters with a kernel (no memset), then runs
- * the GEMM.  All calls on one device share its scratch: calls that may
- * overlap in time on one device (different streams without ordering) race
- * and give wrong results; calls on one stream are safe.
+ * of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  At N = 4096,
+ * K = 12288 (the MLP down projection) that admits M <= 1280; the BASELINE
+ * prefill (M = 3100, 208 tiles, 156 MiB) does not fit and needs
+ * umic_linear_ws_bf16.  The device's first call clears the scratch's
+ * counter region with a kernel (no memset); every launch leaves it cleared.
+ * All calls on one device share its scratch: calls that may overlap in time
+ * on one device (different streams without ordering) may give wrong
+ * results, or make a tile's reduction wait give up after well under a
+ * second and leave that tile unwritten (the scratch's status word, not
+ * readable through this API, is then set); calls on one stream are safe.
  * No counterpart in the reference: an entry point for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that
  * forbid allocation).

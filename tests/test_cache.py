@@ -280,3 +280,63 @@ def test_flow_step_graph_falls_back_to_eager_on_cpu():
     x = torch.randn(2, 3)
     assert torch.equal(model.diffusion.sample(x, step_fn=step_fn), x * 2)
     assert isinstance(model.diffusion.seen[0], FlowStepGraph) and model.diffusion.seen[1] is None
+
+
+def test_repeat_cache_rebinds_to_a_new_cache_object():
+    """A second inference's cache -- freed and rebuilt, same length, possibly
+    at the freed cache's address -- gets a fresh stand-in: the expert sees the
+    new prefix, never the previous inference's KV."""
+    import gc
+
+    from umic.cache import CacheStandIn
+
+    model = text_model(layers=1)
+    seen = []
+
+    class Expert(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.lm = model
+
+        def forward(self, inputs_embeds=None, past_key_values=None):
+            seen.append(past_key_values)
+            return self.lm(inputs_embeds=inputs_embeds, past_key_values=past_key_values,
+                           use_cache=True)
+
+    expert = Expert()
+    integrate.fuse_repeat_cache(expert, extra_tokens_hint=4)
+    integrate.fuse_repeat_cache(expert, extra_tokens_hint=4)   # idempotent
+    assert len(expert._forward_pre_hooks) == 1
+    stand_in = expert._umic_cache_stand_in
+    assert isinstance(stand_in, CacheStandIn)
+
+    def prefix(seed):
+        torch.manual_seed(seed)
+        dyn = DynamicCache()
+        with torch.no_grad():
+            model(inputs_embeds=torch.randn(1, 10, 128).to(BF), past_key_values=dyn,
+                  use_cache=True)
+        return dyn
+
+    step = torch.randn(1, 6, 128).to(BF)
+    dyn = prefix(3)
+    with torch.no_grad():
+        expert(inputs_embeds=step, past_key_values=dyn)
+    first = seen[-1]
+    del dyn
+    gc.collect()
+    dyn2 = prefix(4)
+    want = [lyr.keys.clone() for lyr in dyn2.layers]
+    with torch.no_grad():
+        expert(inputs_embeds=step, past_key_values=dyn2)
+    second = seen[-1]
+    assert second is not first and stand_in.bound_to(dyn2)
+    for lyr, k in zip(second.layers, want):
+        assert torch.equal(lyr.keys[:, :, :10], k)
+    # the same object again: the stand-in is reused and cut back to 10 tokens
+    with torch.no_grad():
+        expert(inputs_embeds=step, past_key_values=dyn2)
+    assert seen[-1] is second and second.get_seq_length() == 16
+    # nothing to stand in for: no cache, a stand-in already, empty layers
+    assert stand_in.resolve(None) is None and stand_in.resolve(second) is None
+    assert stand_in.resolve(DynamicCache()) is None

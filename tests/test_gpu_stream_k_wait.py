@@ -1,0 +1,66 @@
+"""GPU: the stream-K reduction wait is bounded.
+
+A split tile's last-arriving workgroup waits for the tile's other segments
+to publish their partials.  With a workspace whose counters are corrupted
+-- here preset from the host: tile 0's "written" count far past any value
+the launch can produce -- the wait gives up after its spin limit (well
+under a second), records 1 + tile in the workspace's sticky status word
+(UMIC_SK_STATUS_OFFSET), resets the tile's counters and leaves that tile's
+output unwritten; every other tile is computed as usual and the launch
+ends normally.  The workspace is then clean again: with the status word
+cleared, the next call reproduces the clean result bit for bit.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from helpers import bf16_randn
+
+from umic import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+STATUS_OFFSET = 8192  # UMIC_SK_STATUS_OFFSET
+
+
+def _call(x, w, out, ws):
+    M, K = x.shape
+    N = w.shape[0]
+    _lib.call("umic_linear_ws_bf16", x.data_ptr(), w.data_ptr(), None, out.data_ptr(), M, N, K,
+              K, K, N, _lib.UMIC_ACT_NONE, ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+
+
+def test_wait_gives_up_on_a_corrupted_counter():
+    M, N, K = 256, 4096, 12288   # 16 tiles, every one split in two segments
+    need = _lib.lib().umic_linear_workspace_bytes(M, N, K)
+    print(f"stream-K bounded wait M={M} N={N} K={K} ws={need}", flush=True)
+    assert need > STATUS_OFFSET + 4
+    g = torch.Generator().manual_seed(11)
+    x = bf16_randn(M, K, gen=g).to(DEV)
+    w = bf16_randn(N, K, scale=0.02, gen=g).to(DEV)
+    clean_ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    _call(x, w, ref, clean_ws)
+
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    counters = ws[:STATUS_OFFSET].view(torch.int32)   # [arrived, written] per tile
+    status = ws[STATUS_OFFSET:STATUS_OFFSET + 4].view(torch.int32)
+    counters[1] = 1000                                 # tile 0's written count
+    sentinel = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = sentinel.clone()
+    _call(x, w, out, ws)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1                     # tile 0 gave up
+    assert not counters.any()                          # counters reset
+    # tile 0 is the output block rows 0..255, columns 0..255
+    assert torch.equal(out[:, :256], sentinel[:, :256])
+    assert torch.equal(out[:, 256:], ref[:, 256:])
+    assert int(clean_ws[STATUS_OFFSET:STATUS_OFFSET + 4].view(torch.int32).item()) == 0
+
+    status.zero_()
+    out2 = torch.empty_like(out)
+    _call(x, w, out2, ws)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0 and not counters.any()
+    assert torch.equal(out2, ref)

@@ -98,3 +98,34 @@ def test_shape_beyond_the_scratch_is_rejected():
     assert "64 MiB" in _lib.error_string(rc)
     torch.cuda.synchronize()
     assert not out.any()  # nothing ran
+
+
+def test_static_scratch_under_graph_capture():
+    """The static entry point captured in a HIP graph (its callers are code
+    under capture): every replay, with new inputs copied in and eager work
+    between replays, equals the workspace entry point bit for bit."""
+    M, N, K = 300, 4096, 12288
+    print(f"static stream-K graph capture M={M} N={N} K={K}", flush=True)
+    x, w, _ = _operands(M, N, K, 5)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+
+    def launch():
+        _lib.call("umic_linear_sk_static_bf16", x.data_ptr(), w.data_ptr(), None,
+                  out.data_ptr(), M, N, K, K, K, N, _lib.UMIC_ACT_NONE, _lib.stream_of(x))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()                      # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    for seed in (6, 7, 8):
+        x2, _, _ = _operands(M, N, K, seed)
+        x.copy_(x2)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _with_workspace(x, w, None, _lib.UMIC_ACT_NONE)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), seed

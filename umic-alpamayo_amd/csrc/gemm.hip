@@ -516,6 +516,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
 // all-zero counters again after every launch.
 struct SkArgs {
   int* counters;   // [2 * T]: arrived, written (zero between launches)
+  int* status;     // sticky status word (0: every wait completed)
   f32x4_t* slots;  // [T][kSkMaxSeg][kSlotVec]: segment partials
   int T, KT, ks;   // tiles, K steps per tile, main steps per tile
   int G;           // workgroups (T main + G - T tail)
@@ -527,8 +528,24 @@ constexpr int kSkMaxSeg = 3;             // segments per tile (checked on the ho
 // call's slots may overlap another call's counters: with the counter region
 // sized by the call's own tile count, a call with few tiles stored partials
 // where a later call with more tiles kept (and trusted) zero counters.
+// The region also holds one sticky status word after the counters, at byte
+// kSkStatusOffset: a last arriver whose wait gives up (below) stores 1 + its
+// tile index there; nothing else writes it and no launch clears it.
 constexpr int kSkMaxTiles = 1024;        // stream-K needs fewer tiles than CUs
-constexpr int64_t kSkCounterBytes = 2 * kSkMaxTiles * (int64_t)sizeof(int);
+constexpr int64_t kSkStatusOffset = 2 * kSkMaxTiles * (int64_t)sizeof(int);
+constexpr int64_t kSkCounterBytes = kSkStatusOffset + 256;
+static_assert(kSkStatusOffset == UMIC_SK_STATUS_OFFSET, "status word offset of the C ABI");
+static_assert(kSkCounterBytes % 256 == 0, "partial slots stay 256-byte aligned");
+
+// Bound of the last arriver's wait.  The segments it waits for have already
+// arrived, so they are resident and finish their 256 KB partial store within
+// microseconds; a count that never arrives means a corrupted workspace (or
+// calls overlapping on one), and the wait then gives up instead of holding
+// the GPU.  Each poll is one device-scope load (an L2 round trip, about
+// 0.5-1 us under load) plus s_sleep(2) (2 x 64 clocks); 2^19 polls last at
+// least 2^19 x 128 clocks = 28 ms at 2.4 GHz and, with the load latency,
+// well under a second (0.7 s even at a 100 MHz clock without it).
+constexpr int kSkSpinLimit = 1 << 19;
 
 // Tail units: v = t * L + r is step ks + r of tile t (L = KT - ks); tail
 // workgroup j owns [j*Ut/Gt, (j+1)*Ut/Gt), Ut = T*L, Gt = G - T (Ut*Gt < 2^31,
@@ -655,12 +672,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
       if (tid == 0) __hip_atomic_fetch_add(written, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       continue;
     }
-    // Last: wait (device-scope relaxed loads) for the other nseg - 1.
+    // Last: wait (device-scope relaxed loads) for the other nseg - 1, at
+    // most kSkSpinLimit polls.  A wait that gives up records the tile in
+    // the sticky status word, resets the tile's counters and leaves the
+    // tile's output unwritten; the launch still ends normally.
     if (tid == 0) {
-      while (__hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != nseg - 1)
-        __builtin_amdgcn_s_sleep(1);
+      int polls = 0;
+      while (__hip_atomic_load(written, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != nseg - 1 &&
+             ++polls < kSkSpinLimit)
+        __builtin_amdgcn_s_sleep(2);
+      *arrival = polls < kSkSpinLimit;
+      if (polls >= kSkSpinLimit) {
+        __hip_atomic_store(s.status, 1 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(written, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __syncthreads();
+    const bool complete = *arrival;
+    __syncthreads();  // the word is staged output space below
+    if (!complete) continue;
     // The (one or two) other segments, in segment order: o1 < o2.
     const int o1 = seg == 0 ? 1 : 0;
     const int o2 = seg == 2 ? 1 : 2;
@@ -1009,7 +1040,7 @@ int launch_gemm_sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
   // whole tile columns, m fastest: down_proj at M = 3100 ran 266-269 us
   // against 280-282 us with groups of four tile rows (one process)
   g.gm = g.tiles_m;
-  SkArgs s{static_cast<int*>(ws),
+  SkArgs s{static_cast<int*>(ws), reinterpret_cast<int*>(static_cast<char*>(ws) + kSkStatusOffset),
            reinterpret_cast<f32x4_t*>(static_cast<char*>(ws) + pl.counter_bytes), (int)pl.tiles,
            pl.KT, pl.ks, pl.G};
   const int64_t grid = ((pl.G + 7) / 8) * 8;
@@ -1046,8 +1077,9 @@ constexpr int kScratchDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 // The device address of `scratch` on the current device, looked up once per
-// device with that device current; 0 or a hipError_t value.
-int scratch_address(void** out) {
+// device with that device current; 0 or a hipError_t value.  *first is true
+// for the one call that looked the address up on this device.
+int scratch_address(void** out, bool* first) {
   static std::mutex mu;
   static void* addr[kScratchDevices];
   int dev = 0;
@@ -1055,6 +1087,7 @@ int scratch_address(void** out) {
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kScratchDevices) return UMIC_ERR_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(mu);
+  *first = !addr[dev];
   if (!addr[dev]) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -1168,16 +1201,22 @@ extern "C" int umic_linear_sk_static_bf16(const void* x, const void* w, const vo
     return umic_linear_bf16(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, stream);
   if (pl.bytes > kScratchBytes) return UMIC_ERR_SCRATCH;
   void* ws = nullptr;
-  rc = scratch_address(&ws);
+  bool first = false;
+  rc = scratch_address(&ws, &first);
   if (rc != UMIC_OK) return rc;
-  // The counters start at zero on every call, whatever an earlier call on
-  // this device left behind.
   hipStream_t st = as_stream(stream);
-  const int n = (int)(2 * pl.tiles);
-  hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                     static_cast<int*>(ws), n);
-  rc = launch_status();
-  if (rc != UMIC_OK) return rc;
+  // The counter region (tile counters and the status word) is cleared once,
+  // ahead of the device's first stream-K launch on it; every launch leaves
+  // the counters at zero, so later calls find them cleared.  Clearing on
+  // every call instead would zero counters that a call still running on
+  // another stream is waiting on.
+  if (first) {
+    const int n = (int)(kSkCounterBytes / sizeof(int));
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<int*>(ws), n);
+    rc = launch_status();
+    if (rc != UMIC_OK) return rc;
+  }
   return run_linear_sk(x, w, bias, out, M, N, K, ldx, ldw, ldo, act, pl, ws, st);
 }
 

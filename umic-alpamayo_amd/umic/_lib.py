@@ -8,8 +8,8 @@ owner -- no torch types cross the boundary.
 
 ``HAS_KERNELS`` is True once the library has loaded (it loads lazily on first
 use, or eagerly via :func:`load`).  A wrapper called on device tensors while
-the library is missing raises :class:`UmicLibraryError`: the fused path never
-degrades silently to something else.
+the library is missing raises :class:`UmicLibraryError`; the injection layer
+checks :func:`available` first and patches nothing when it is False.
 """
 
 from __future__ import annotations
@@ -116,6 +116,11 @@ def available() -> bool:
         return True
     except UmicLibraryError:
         return False
+
+
+def load_error() -> str | None:
+    """Why the last load attempt failed (None if it has not failed)."""
+    return _load_error
 
 
 def lib() -> ctypes.CDLL:

@@ -27,9 +27,12 @@ so mask and attention back-end selection are unchanged.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 from transformers.cache_utils import DynamicCache, DynamicLayer
 
+from umic import _lib
 from umic.kernels import rope
 
 
@@ -52,7 +55,7 @@ class KVArena:
         self.cursor: torch.Tensor | None = None
         self.window = 0
         # the buffers never move: check once whether the fused append can write them
-        self.fused_ok = rope.kv_cache_ok(self.k(0), self.v(0))
+        self.fused_ok = rope.kv_cache_ok(self.k(0), self.v(0)) and _lib.available()
 
     @property
     def capacity(self) -> int:
@@ -251,3 +254,47 @@ class InplaceKVCache(DynamicCache):
         if layer_idx >= len(self.layers):
             return 0
         return self.layers[layer_idx].get_seq_length()
+
+
+class CacheStandIn:
+    """The ``InplaceKVCache`` that stands in for a caller's ``DynamicCache``
+    across the calls of an append-then-crop loop (a flow expert's denoising
+    steps, a decode loop).
+
+    The caller keeps its own cache and crops it back to the prefix after
+    every step.  ``resolve(source, n_new)`` returns the stand-in for
+    ``source``: built (one copy into an arena with room for the step's new
+    tokens) the first time that cache object is seen, and thereafter only
+    cut back to ``source``'s length, an O(1) crop that makes the caller's
+    own crop redundant.  The source is held by a weak reference and compared
+    by identity, so a later cache -- even one CPython places at a freed
+    cache's address -- is never mistaken for the one converted before.
+    ``None`` means "leave the call alone": no cache, a stand-in already, or
+    a cache whose layers are not all populated yet (generate() creates
+    them empty before prefill).
+    """
+
+    def __init__(self, extra_tokens: int = 64) -> None:
+        self.extra_tokens = extra_tokens
+        self._source: weakref.ref | None = None
+        self._inplace: InplaceKVCache | None = None
+
+    @staticmethod
+    def convertible(cache) -> bool:
+        if not isinstance(cache, DynamicCache) or isinstance(cache, InplaceKVCache):
+            return False
+        layers = getattr(cache, "layers", None)
+        return bool(layers) and all(getattr(lyr, "keys", None) is not None for lyr in layers)
+
+    def bound_to(self, cache) -> bool:
+        return self._source is not None and self._source() is cache
+
+    def resolve(self, source, n_new: int = 0) -> "InplaceKVCache | None":
+        if not self.convertible(source):
+            return None
+        if not self.bound_to(source):
+            self._inplace = InplaceKVCache.from_dynamic(
+                source, extra_tokens=max(n_new, self.extra_tokens))
+            self._source = weakref.ref(source)
+        self._inplace.crop(source.get_seq_length())
+        return self._inplace

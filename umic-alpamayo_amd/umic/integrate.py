@@ -16,9 +16,14 @@ regimes -- the tiled kernel from its TILED_MIN_ROWS_* bound (at least
 FUSE_MIN_ROWS), the decode GEMV up to its GEMV_ROWS_* bound; and no
 gradient to carry, since the kernels have no backward).  If not, it runs
 the module's own class forward -- the original eager math on whatever
-device the inputs live on, recorded by autograd as usual.  If the inputs are eligible but libumic_hip.so
-is missing, the kernel wrapper raises: the fused path never degrades
-silently.
+device the inputs live on, recorded by autograd as usual.
+
+Without the kernel library (libumic_hip.so missing or unloadable) every
+fuser is a no-op, as the reference's fusers are without their kernel
+backend (src/umic/integrate.py:653-655, 673-675): nothing is patched, the
+fuser reports 0 / False with one warning, and the model keeps its eager
+forwards.  The kernel wrappers called directly still raise
+UmicLibraryError.
 """
 
 from __future__ import annotations
@@ -28,10 +33,23 @@ import logging
 import torch
 from torch import nn
 
+from umic import _lib
 from umic.kernels import fused_ffn, layernorm, linear, rmsnorm, rope
 from umic.kernels._common import grad_needed
 
 logger = logging.getLogger(__name__)
+
+
+def _backend_ready(fuser: str) -> bool:
+    """True when libumic_hip.so loads.  Otherwise the named fuser patches
+    nothing and reports 0 / False (the reference's no-backend behaviour,
+    src/umic/integrate.py:653-655): a patched forward would otherwise raise
+    at the model's first eligible call."""
+    if _lib.available():
+        return True
+    logger.warning("%s: kernel library unavailable (%s); nothing patched", fuser,
+                   _lib.load_error())
+    return False
 
 _SILU_NAMES = ("silu", "swish")
 
@@ -185,6 +203,8 @@ def fuse_mlps(model: nn.Module, dry_run: bool = False) -> int:
     Returns:
         Number of modules matched (and patched unless dry_run).
     """
+    if not _backend_ready("fuse_mlps"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         if _is_p5_mlp(module):
@@ -217,6 +237,8 @@ def fuse_linears(model: nn.Module, names: tuple[str, ...] = INEFFICIENT_LINEAR_N
     Returns:
         Number of Linear modules matched (and patched unless dry_run).
     """
+    if not _backend_ready("fuse_linears"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         leaf = name.rsplit(".", 1)[-1]
@@ -249,6 +271,8 @@ def fuse_rmsnorms(model: nn.Module, dry_run: bool = False) -> int:
     Returns:
         Number of modules matched (and patched unless dry_run).
     """
+    if not _backend_ready("fuse_rmsnorms"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         if "rmsnorm" not in type(module).__name__.lower():
@@ -335,6 +359,8 @@ def fuse_add_rmsnorm(model: nn.Module, dry_run: bool = False) -> int:
     Returns:
         Number of decoder layers matched (and patched unless dry_run).
     """
+    if not _backend_ready("fuse_add_rmsnorm"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         if not _is_residual_decoder_layer(module):
@@ -361,6 +387,8 @@ def _patched_layernorm_forward(self: nn.LayerNorm, x: torch.Tensor) -> torch.Ten
 
 def fuse_layernorms(model: nn.Module, dry_run: bool = False) -> int:
     """Swap forward of nn.LayerNorm modules (last-dim, affine with bias)."""
+    if not _backend_ready("fuse_layernorms"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         if (isinstance(module, nn.LayerNorm) and len(module.normalized_shape) == 1
@@ -459,6 +487,8 @@ def fuse_gelu_mlps(model: nn.Module, dry_run: bool = False) -> int:
     Returns:
         Number of modules matched (and patched unless dry_run).
     """
+    if not _backend_ready("fuse_gelu_mlps"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         match = _is_gelu_mlp(module)
@@ -615,6 +645,8 @@ def fuse_vision_encoder_pipeline(model: nn.Module, dry_run: bool = False) -> int
         out_cls = getattr(mod, "BaseModelOutputWithDeepstackFeatures", None)
     except ImportError:
         out_cls = None
+    if not _backend_ready("fuse_vision_encoder_pipeline"):
+        return 0
     count = 0
     for name, module in model.named_modules():
         if not _is_deepstack_vision_encoder(module):
@@ -653,6 +685,8 @@ def fuse_vision_rope() -> bool:
     if mod is None:
         logger.warning("fuse_vision_rope: qwen3_vl module not found")
         return False
+    if not _backend_ready("fuse_vision_rope"):
+        return False
     cur = mod.apply_rotary_pos_emb_vision
     if getattr(cur, "_umic_fused", False):
         return True
@@ -674,6 +708,8 @@ def fuse_text_rope() -> bool:
     mod = _qwen3_vl_module()
     if mod is None:
         logger.warning("fuse_text_rope: qwen3_vl module not found")
+        return False
+    if not _backend_ready("fuse_text_rope"):
         return False
     cur = mod.apply_rotary_pos_emb
     if getattr(cur, "_umic_fused", False):
@@ -834,6 +870,8 @@ def fuse_kv_rope(model: nn.Module, dry_run: bool = False) -> int:
     if _qwen3_vl_module() is None:
         logger.warning("fuse_kv_rope: qwen3_vl module not found")
         return 0
+    if not _backend_ready("fuse_kv_rope"):
+        return 0
     count = 0
     for _, module in model.named_modules():
         if not _is_text_attention(module):
@@ -849,43 +887,32 @@ def fuse_kv_rope(model: nn.Module, dry_run: bool = False) -> int:
 def fuse_repeat_cache(repeat_module: nn.Module, extra_tokens_hint: int = 64) -> None:
     """Replace per-step KV concatenation in append-then-crop loops.
 
-    Same contract as the reference (src/umic/integrate.py:715-756): a
-    forward pre-hook on `repeat_module` converts the first fully populated
-    DynamicCache it is given into an ``InplaceKVCache`` once, and on every
-    call re-syncs the substitute's write pointer to the caller's cache
-    length (an O(1) crop), so the caller's own ``crop()`` becomes redundant.
+    Contract of the reference (src/umic/integrate.py:715-756): after this,
+    every call of `repeat_module` that passes a populated DynamicCache as
+    ``past_key_values`` runs on an ``InplaceKVCache`` standing in for it --
+    converted once per cache object, and cut back to that cache's length
+    before each call -- so the loop's per-step concatenation and crop copy
+    nothing.  The decision is ``umic.cache.CacheStandIn.resolve``; the
+    forward pre-hook installed here only swaps the argument.  Idempotent.
     """
-    from transformers.cache_utils import DynamicCache
-
-    from umic.cache import InplaceKVCache
+    from umic.cache import CacheStandIn
 
     if getattr(repeat_module, "_umic_repeat_cache_hook", None) is not None:
-        return                                   # installed already: idempotent
-    state: dict[str, object] = {"orig_id": None, "converted": None}
+        return
+    stand_in = CacheStandIn(extra_tokens_hint)
 
-    def _pre_hook(module, args, kwargs):
-        pkv = kwargs.get("past_key_values")
-        if pkv is None or isinstance(pkv, InplaceKVCache):
-            return None
-        if not isinstance(pkv, DynamicCache) or not getattr(pkv, "layers", None):
-            return None
-        # generate() creates the cache with lazy (keys=None) layers before
-        # prefill: convert only once every layer holds KV
-        if any(getattr(lyr, "keys", None) is None for lyr in pkv.layers):
-            return None
+    def _swap_cache(module, args, kwargs):
         emb = kwargs.get("inputs_embeds")
-        n_new = emb.shape[1] if emb is not None else 0
-        if state["orig_id"] != id(pkv):
-            state["orig_id"] = id(pkv)
-            state["converted"] = InplaceKVCache.from_dynamic(
-                pkv, extra_tokens=max(n_new, extra_tokens_hint))
-        conv = state["converted"]
-        conv.crop(pkv.get_seq_length())
-        kwargs["past_key_values"] = conv
+        inplace = stand_in.resolve(kwargs.get("past_key_values"),
+                                   emb.shape[1] if emb is not None else 0)
+        if inplace is None:
+            return None
+        kwargs["past_key_values"] = inplace
         return args, kwargs
 
+    repeat_module._umic_cache_stand_in = stand_in
     repeat_module._umic_repeat_cache_hook = repeat_module.register_forward_pre_hook(
-        _pre_hook, with_kwargs=True)
+        _swap_cache, with_kwargs=True)
     logger.info("fuse_repeat_cache: hook installed on %s", type(repeat_module).__name__)
 
 

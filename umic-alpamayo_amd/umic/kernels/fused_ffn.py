@@ -72,9 +72,10 @@ def gate_silu_mul_hip(x: torch.Tensor, w_gate: torch.Tensor,
 
 
 def gate_silu_mul(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
-    """Best implementation for the P5 motif: the HIP kernel for GPU tensors
-    (raising if libumic_hip.so is missing), the eager chain for CPU tensors."""
-    if x.is_cuda:
+    """Best available implementation for the P5 motif (reference
+    src/umic/kernels/fused_ffn.py:121-126): the HIP kernel for GPU tensors
+    when libumic_hip.so loads, else the eager chain."""
+    if x.is_cuda and _lib.available():
         return gate_silu_mul_hip(x, w_gate, w_up)
     return gate_silu_mul_eager(x, w_gate, w_up)
 
