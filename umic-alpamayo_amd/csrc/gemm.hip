@@ -44,6 +44,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 namespace umic {
@@ -496,6 +497,323 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   p.bind(g, m0, n0);
   p.run(lds, 0, (int)(g.K / kBK));
   p.template store<ACT, BIAS>(lds, g, m0, n0);
+}
+
+// ---- Four-wave core (K a multiple of 64) ---------------------------------
+//
+// The data-parallel kernel for K % 64 == 0.  Same tile (256 x rows by 256
+// weight rows), tile order, operand layout and arithmetic as gemm_kernel --
+// every output is bit-identical to it -- with a different division of the
+// tile and K loop:
+//
+// Waves.  Four wavefronts, one per SIMD.  Wave w owns a 128 x 128 block
+// (x rows from wm * 128, weight rows from wn * 128; for P5 64 gate rows and
+// the same 64 up rows), 8 x 8 blocks of v_mfma_f32_16x16x32_bf16 with its
+// 256 fp32 accumulators in AGPRs.  Per 32 of K a wave reads 16 fragments
+// for 64 MFMAs (gemm_kernel's waves read 12 for 32): a third fewer LDS
+// reads per MFMA.
+//
+// MFMAs as inline asm.  Each MFMA is issued with its accumulator as a tied
+// "+a" operand, so the accumulator stays in one AGPR for the whole tile.
+// Left to the compiler, 256 live accumulators in a 256-entry AGPR file were
+// renamed and copied (v_accvgpr_read/write/mov) between MFMAs -- 236 copies
+// per 128 MFMAs.  The compiler's hazard tracking does not see into asm, so
+// the kernel supplies the two wait states it needs itself: the tile's first
+// MFMAs take srcC = 0 (no accumulator initialisation to wait for), and the
+// reads of the results come after 32 wait states in asm statements that take
+// every accumulator as an operand (nothing can be moved above them).
+//
+// Stages of K = 64.  A staged row is 128 bytes, a whole cache line, and one
+// direct-to-LDS wave load moves 8 rows of it: the requests are whole lines
+// (gemm_kernel's 32-deep stages move half lines).  Two stages of 64 KB
+// fill 128 KB of LDS.  Stage j's first half (32 of K) runs its 64 MFMAs
+// while the wave reads its fragments of the second half; then each wave
+// waits for its own loads of stage j+1 and the block meets at a barrier
+// (everyone's loads have landed, everyone's reads of stage j are done);
+// the second half runs its MFMAs while the wave loads stage j+2 into stage
+// j's buffer and reads its fragments of stage j+1.  One barrier per 64 of
+// K; loads are issued one stage (128 MFMAs per wave) ahead.  Rows are
+// XOR-swizzled by (row >> 1) & 7 (16-byte chunks within the 128-byte row):
+// measured 2-3% bank-conflict cycles against 37-43% unswizzled.
+//
+// Dead fragments.  A wave whose x rows lie (partly) past the tile's live
+// rows runs the K loop instantiated for its count of live fragments
+// (0..8), so the last row tile of M = 3100 and the even 240-row tiles of a
+// multi-round launch multiply no zero rows; every instantiation issues the
+// same loads and meets the same barriers.
+constexpr int kW4Threads = 256;
+constexpr int kW4BK = 64;                        // K per stage
+constexpr int kW4Row = kW4BK * 2;                // staged bytes per row
+constexpr int kW4OpBytes = kBW * kW4Row;         // one operand of a stage (32 KB)
+constexpr int kW4StageBytes = 2 * kW4OpBytes;    // 64 KB
+constexpr int kW4LdsBytes = 160 * 1024;          // two stages; the staged output needs 135 KB
+
+__device__ __forceinline__ int w4_swz(int row) { return (row >> 1) & 7; }
+
+// s_waitcnt vmcnt(VM) lgkmcnt(LGKM) through the builtin, so the compiler's
+// own waitcnt pass sees the counters it clears (an asm s_waitcnt left it
+// assuming LDS reads were still in flight, and it added waits of its own
+// before the next MFMAs); the empty asm statements keep memory accesses
+// from moving across.
+template <int VM, int LGKM>
+__device__ __forceinline__ void w4_wait() {
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "waitcnt fields");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (LGKM << 8) | ((VM >> 4) << 14));
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void w4_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int NB>
+struct W4Tile {
+  lds_char* lds;
+  int wave, wm, wn, frow, fch;
+  int fo0, fo1;      // a lane's fragment offset inside a 16-row block, K halves 0 / 1
+  int xbase;         // first x row of this wave's fragments
+  __amdgpu_buffer_rsrc_t rx, rw;
+  int xoff0, xoff1, woff0, woff1;  // per-lane load offsets (row, chunk) for even / odd loads
+  int xstep, wstep;                // bytes between 8-row load groups (wave-uniform)
+  f32x4_t acc[8][8];
+  bf16x8_t fa[2][8], fb[2][8];
+
+  // Weight row of fragment block a: linear wn*128 + a*16; P5 gate rows
+  // wn*64 + a*16 (a < 4) and the matching up rows 128 + wn*64 + (a-4)*16.
+  __device__ __forceinline__ int arow(int a) const {
+    return NB == 1 ? wn * 128 + a * 16 : (a >> 2) * 128 + wn * 64 + (a & 3) * 16;
+  }
+
+  // Load q (0..15) of a stage: 0..7 the weight rows wave*64 + q*8 .. + 8,
+  // 8..15 the x rows wave*64 + (q-8)*8 .. + 8 (rows past the tile's own, or
+  // past M / N, read as range-checked zeros).  Lane l writes LDS slot l % 8
+  // of row l / 8, so it fetches the 16-byte chunk the swizzle puts there.
+  __device__ __forceinline__ void issue(int stage, int k, int q) {
+    lds_char* d = lds + stage * kW4StageBytes + (q >> 3) * kW4OpBytes +
+                  (wave * 64 + (q & 7) * 8) * kW4Row;
+    if (q < 8)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)d, 16, (q & 1) ? woff1 : woff0,
+                                               k * 2 + (q & 7) * wstep, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)d, 16, (q & 1) ? xoff1 : xoff0,
+                                               k * 2 + (q & 7) * xstep, 0, 0);
+  }
+
+  // Fragment f (0..7: weight blocks, 8..15: x blocks) of K half h of a stage.
+  __device__ __forceinline__ void read(int buf, int stage, int h, int f) {
+    const lds_char* base = lds + stage * kW4StageBytes + (h ? fo1 : fo0);
+    if (f < 8)
+      fa[buf][f] = *(const bf16x8_t*)(base + arow(f) * kW4Row);
+    else
+      fb[buf][f - 8] = *(const bf16x8_t*)(base + kW4OpBytes + (xbase + (f - 8) * 16) * kW4Row);
+  }
+
+  // The 8 x NBX MFMAs of one K half on fragment buffer B; body(i) places
+  // memory work after MFMA i.  ZERO: the tile's first half, srcC = 0.
+  template <int NBX, int B, bool ZERO, typename Body>
+  __device__ __forceinline__ void mfmas(Body body) {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int a = i >> 3, b = i & 7;
+      if (b < NBX) {
+        if constexpr (ZERO)
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                       : "=a"(acc[a][b]) : "v"(fa[B][a]), "v"(fb[B][b]));
+        else
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                       : "+a"(acc[a][b]) : "v"(fa[B][a]), "v"(fb[B][b]));
+      }
+      body(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // The K loop over n stages (stages 0 and 1 already in flight, stage 0
+  // landed block-wide).  Returns with every load landed and every MFMA
+  // result readable.
+  template <int NBX>
+  __device__ __forceinline__ void kloop(int n) {
+    constexpr bool kAny = NBX > 0;
+    auto wanted = [](int f) { return kAny && (f < 8 || f - 8 < NBX); };
+#pragma unroll
+    for (int f = 0; f < 16; ++f)
+      if (wanted(f)) read(0, 0, 0, f);
+    w4_wait<63, 0>();
+    // Stage j; stage 0 (ZERO) is peeled off the loop, so every accumulator
+    // has one definition reaching the loop and keeps its register.
+    auto stage = [&](int j, auto zero) {
+      const int sj = j & 1, sn = sj ^ 1;
+      mfmas<NBX, 0, decltype(zero)::value>([&](int i) {
+        if (i >= 1 && i < 17 && wanted(i - 1)) read(1, sj, 1, i - 1);
+      });
+      w4_wait<0, 0>();
+      w4_barrier();
+      // Past the last stage the refills read in-range data or range-checked
+      // zeros, and the reads take fragments that are never used.
+      mfmas<NBX, 1, false>([&](int i) {
+        if (i % 4 == 1) issue(sj, (j + 2) * kW4BK, i / 4);
+        if (i >= 2 && i < 18 && wanted(i - 2)) read(0, sn, 0, i - 2);
+      });
+      w4_wait<63, 0>();
+    };
+    stage(0, std::true_type{});
+    for (int j = 1; j < n; ++j) stage(j, std::false_type{});
+    w4_wait<0, 0>();
+    w4_barrier();
+    // The MFMA results are read below: 32 wait states, in statements that
+    // take every accumulator, so no read moves above them.
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      if (a == 0)
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                     : "+a"(acc[a][0]), "+a"(acc[a][1]), "+a"(acc[a][2]), "+a"(acc[a][3]),
+                       "+a"(acc[a][4]), "+a"(acc[a][5]), "+a"(acc[a][6]), "+a"(acc[a][7]));
+      else
+        asm volatile(""
+                     : "+a"(acc[a][0]), "+a"(acc[a][1]), "+a"(acc[a][2]), "+a"(acc[a][3]),
+                       "+a"(acc[a][4]), "+a"(acc[a][5]), "+a"(acc[a][6]), "+a"(acc[a][7]));
+    }
+  }
+
+  static constexpr int kOutCols = NB == 1 ? kBW : kBW / 2;
+  static constexpr int kOutRow = kOutCols * 2 + 16;  // staged bytes per output row
+  static_assert(kBM * kOutRow <= kW4LdsBytes, "staged tile must fit the LDS");
+
+  // Stage the tile's live fragments as bf16 rows in LDS (bias, GELU or
+  // silu(g) * u in fp32, one rounding), as gemm_kernel's epilogue.
+  template <int NBX, int ACT, bool BIAS>
+  __device__ __forceinline__ void stage_out(const GemmArgs& g, int n0) {
+    constexpr int kOutBlocks = NB == 1 ? 8 : 4;
+    char* out = (char*)lds;
+#pragma unroll
+    for (int a = 0; a < kOutBlocks; ++a) {
+      const int col = (NB == 1 ? arow(a) : wn * 64 + a * 16) + fch * 4;
+      f32x4_t bias = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (NB == 1 && BIAS) {
+        if (n0 + col < g.N) {
+          const uint2 bw = *reinterpret_cast<const uint2*>(g.bias + n0 + col);
+          bias[0] = bf_lo(bw.x);
+          bias[1] = bf_hi(bw.x);
+          bias[2] = bf_lo(bw.y);
+          bias[3] = bf_hi(bw.y);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NBX; ++b) {
+        const f32x4_t v = acc[a][b];
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = v[e];
+          if constexpr (NB == 2) {
+            const float den = 1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+            x = x * __builtin_amdgcn_rcpf(den) * acc[a + 4][b][e];
+          } else {
+            if constexpr (BIAS) x = x + bias[e];
+            if constexpr (ACT == UMIC_ACT_GELU) x = gelu_erf(x);
+            if constexpr (ACT == UMIC_ACT_GELU_TANH) x = gelu_tanh(x);
+          }
+          o[e] = x;
+        }
+        uint2 pk;
+        pk.x = pack2(o[0], o[1]);
+        pk.y = pack2(o[2], o[3]);
+        *reinterpret_cast<uint2*>(out + (xbase + b * 16 + frow) * kOutRow + col * 2) = pk;
+        __builtin_amdgcn_sched_barrier(0);  // one block's reads at a time
+      }
+    }
+  }
+};
+
+template <int NB, int NBX, int ACT, bool BIAS>
+__device__ __forceinline__ void w4_tile(W4Tile<NB>& c, const GemmArgs& g, int n, int n0) {
+  c.template kloop<NBX>(n);
+  c.template stage_out<NBX, ACT, BIAS>(g, n0);
+}
+
+template <int NB, int ACT, bool BIAS>
+__global__ __launch_bounds__(kW4Threads, 1) void gemm_w4_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) char smem[kW4LdsBytes];
+  const int t = xcd_remap(g.tiles);
+  if (t >= g.tiles) return;
+  int m0, n0;
+  tile_origin(g, t, NB == 1 ? kBW : kBW / 2, m0, n0);
+
+  W4Tile<NB> c;
+  c.lds = (lds_char*)smem;
+  const int lane = threadIdx.x & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  c.wm = c.wave & 1;
+  c.wn = c.wave >> 1;
+  c.frow = lane & 15;
+  c.fch = lane >> 4;
+  // the tile owns x rows [m0, mlim); x rows past it read as zero
+  const int64_t mlim = std::min<int64_t>(g.M, (int64_t)m0 + g.bm);
+  const bool up = NB == 2 && c.wave >= 2;
+  const uint16_t* wsrc = up ? g.w1 : g.w0;
+  const int64_t ldw = up ? g.ldw1 : g.ldw0;
+  const int wrow0 = NB == 1 ? n0 + c.wave * 64 : n0 + (c.wave & 1) * 64;
+  c.rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(mlim * g.ldx * 2),
+                                           0x00020000);
+  c.rw = __builtin_amdgcn_make_buffer_rsrc((void*)wsrc, (short)0, (int)(g.N * ldw * 2),
+                                           0x00020000);
+  // staged row wave*64 + q*8 + lr: its swizzle depends on lr and q's parity
+  const int lr = lane >> 3, lc = lane & 7;
+  const int c0 = (lc ^ w4_swz(lr)) * 16, c1 = (lc ^ w4_swz(8 + lr)) * 16;
+  const int xoff = (int)((int64_t)(m0 + c.wave * 64 + lr) * g.ldx * 2);
+  const int woff = (int)((int64_t)(wrow0 + lr) * ldw * 2);
+  c.xoff0 = xoff + c0;
+  c.xoff1 = xoff + c1;
+  c.woff0 = woff + c0;
+  c.woff1 = woff + c1;
+  c.xstep = __builtin_amdgcn_readfirstlane((int)(8 * g.ldx * 2));
+  c.wstep = __builtin_amdgcn_readfirstlane((int)(8 * ldw * 2));
+  // a fragment's 16 rows start at a multiple of 16: the swizzle of its
+  // rows depends on the lane only
+  c.fo0 = c.frow * kW4Row + ((c.fch ^ w4_swz(c.frow)) * 16);
+  c.fo1 = c.frow * kW4Row + (((4 + c.fch) ^ w4_swz(c.frow)) * 16);
+  // x fragments: wave pair wm takes rows [wm * 128, ...) of the tile
+  c.xbase = c.wm * 128;
+  const int live = (int)(mlim - m0) - c.xbase;
+  const int nbx = __builtin_amdgcn_readfirstlane(live <= 0 ? 0 : min(8, (live + 15) / 16));
+  const int n = (int)(g.K / kW4BK);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) c.issue(0, 0, q);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) c.issue(1, kW4BK, q);
+  w4_wait<16, 0>();  // this wave's loads of stage 0
+  w4_barrier();      // everyone's
+  switch (nbx) {
+    case 8: w4_tile<NB, 8, ACT, BIAS>(c, g, n, n0); break;
+    case 7: w4_tile<NB, 7, ACT, BIAS>(c, g, n, n0); break;
+    case 6: w4_tile<NB, 6, ACT, BIAS>(c, g, n, n0); break;
+    case 5: w4_tile<NB, 5, ACT, BIAS>(c, g, n, n0); break;
+    case 4: w4_tile<NB, 4, ACT, BIAS>(c, g, n, n0); break;
+    case 3: w4_tile<NB, 3, ACT, BIAS>(c, g, n, n0); break;
+    case 2: w4_tile<NB, 2, ACT, BIAS>(c, g, n, n0); break;
+    case 1: w4_tile<NB, 1, ACT, BIAS>(c, g, n, n0); break;
+    default: w4_tile<NB, 0, ACT, BIAS>(c, g, n, n0); break;
+  }
+  // Stream the staged tile out as whole rows of 16-byte stores.
+  __syncthreads();
+  constexpr int kOutCols = W4Tile<NB>::kOutCols;
+  constexpr int kOutRow = W4Tile<NB>::kOutRow;
+  constexpr int kChunks = kOutCols / 8;
+  constexpr int kRowsPerPass = kW4Threads / kChunks;
+  const int cc = threadIdx.x % kChunks;
+  const int64_t col = n0 + cc * 8;
+  if (col < g.N) {
+#pragma unroll 4
+    for (int r = threadIdx.x / kChunks; r < kBM; r += kRowsPerPass) {
+      const int64_t m = (int64_t)m0 + r;
+      if (m >= mlim) break;
+      *reinterpret_cast<u32x4*>(g.out + m * g.ldo + col) =
+          *reinterpret_cast<const u32x4*>(smem + r * kOutRow + cc * 16);
+    }
+  }
 }
 
 // Stream-K linear, K-aligned.  With T tiles < G workgroups (one per CU),
@@ -980,7 +1298,12 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
   g.bm = rounds ? tile_rows(g.M) : kBM;
   g.gm = rounds ? kGroupMRounds : kGroupMOne;
   const int64_t grid = ((g.tiles + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st, g);
+  if (g.K % kW4BK == 0)
+    hipLaunchKernelGGL((gemm_w4_kernel<NB, ACT, BIAS>), dim3((unsigned)grid), dim3(kW4Threads), 0,
+                       st, g);
+  else
+    hipLaunchKernelGGL((gemm_kernel<NB, ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st,
+                       g);
   return launch_status();
 }
 
