@@ -569,17 +569,67 @@ __device__ __forceinline__ void w4_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Where one tile's operand rows come from: the buffer resources (x rows past
+// the tile's own, and rows past N, read as zero) and a lane's byte offsets
+// (row, swizzled chunk) for its even and odd loads.
+struct W4Src {
+  __amdgpu_buffer_rsrc_t rx, rw;
+  int xoff0, xoff1, woff0, woff1;
+};
+
 template <int NB>
 struct W4Tile {
   lds_char* lds;
   int wave, wm, wn, frow, fch;
   int fo0, fo1;      // a lane's fragment offset inside a 16-row block, K halves 0 / 1
   int xbase;         // first x row of this wave's fragments
-  __amdgpu_buffer_rsrc_t rx, rw;
-  int xoff0, xoff1, woff0, woff1;  // per-lane load offsets (row, chunk) for even / odd loads
-  int xstep, wstep;                // bytes between 8-row load groups (wave-uniform)
+  W4Src src;         // the tile being loaded
+  int xstep, wstep;  // bytes between 8-row load groups (wave-uniform)
   f32x4_t acc[8][8];
   bf16x8_t fa[2][8], fb[2][8];
+
+  // Lane-invariant set-up (everything but the tile).
+  __device__ __forceinline__ void init(void* smem, const GemmArgs& g) {
+    lds = (lds_char*)smem;
+    const int lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave & 1;
+    wn = wave >> 1;
+    frow = lane & 15;
+    fch = lane >> 4;
+    // a fragment's 16 rows start at a multiple of 16: the swizzle of its
+    // rows depends on the lane only
+    fo0 = frow * kW4Row + ((fch ^ w4_swz(frow)) * 16);
+    fo1 = frow * kW4Row + (((4 + fch) ^ w4_swz(frow)) * 16);
+    xbase = wm * 128;  // wave pair wm takes x rows [wm * 128, ...) of the tile
+    const bool up = NB == 2 && wave >= 2;
+    xstep = __builtin_amdgcn_readfirstlane((int)(8 * g.ldx * 2));
+    wstep = __builtin_amdgcn_readfirstlane((int)(8 * (up ? g.ldw1 : g.ldw0) * 2));
+  }
+
+  // The load addressing of the tile at (m0, n0) owning x rows [m0, mlim).
+  __device__ __forceinline__ W4Src bind(const GemmArgs& g, int m0, int n0, int64_t mlim) const {
+    const int lane = threadIdx.x & 63;
+    const bool up = NB == 2 && wave >= 2;
+    const uint16_t* wsrc = up ? g.w1 : g.w0;
+    const int64_t ldw = up ? g.ldw1 : g.ldw0;
+    const int wrow0 = NB == 1 ? n0 + wave * 64 : n0 + (wave & 1) * 64;
+    W4Src r;
+    r.rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(mlim * g.ldx * 2),
+                                             0x00020000);
+    r.rw = __builtin_amdgcn_make_buffer_rsrc((void*)wsrc, (short)0, (int)(g.N * ldw * 2),
+                                             0x00020000);
+    // staged row wave*64 + q*8 + lr: its swizzle depends on lr and q's parity
+    const int lr = lane >> 3, lc = lane & 7;
+    const int c0 = (lc ^ w4_swz(lr)) * 16, c1 = (lc ^ w4_swz(8 + lr)) * 16;
+    const int xoff = (int)((int64_t)(m0 + wave * 64 + lr) * g.ldx * 2);
+    const int woff = (int)((int64_t)(wrow0 + lr) * ldw * 2);
+    r.xoff0 = xoff + c0;
+    r.xoff1 = xoff + c1;
+    r.woff0 = woff + c0;
+    r.woff1 = woff + c1;
+    return r;
+  }
 
   // Weight row of fragment block a: linear wn*128 + a*16; P5 gate rows
   // wn*64 + a*16 (a < 4) and the matching up rows 128 + wn*64 + (a-4)*16.
@@ -591,16 +641,17 @@ struct W4Tile {
   // 8..15 the x rows wave*64 + (q-8)*8 .. + 8 (rows past the tile's own, or
   // past M / N, read as range-checked zeros).  Lane l writes LDS slot l % 8
   // of row l / 8, so it fetches the 16-byte chunk the swizzle puts there.
-  __device__ __forceinline__ void issue(int stage, int k, int q) {
+  __device__ __forceinline__ void issue(const W4Src& r, int stage, int k, int q) {
     lds_char* d = lds + stage * kW4StageBytes + (q >> 3) * kW4OpBytes +
                   (wave * 64 + (q & 7) * 8) * kW4Row;
     if (q < 8)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)d, 16, (q & 1) ? woff1 : woff0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.rw, (lds_void*)d, 16, (q & 1) ? r.woff1 : r.woff0,
                                                k * 2 + (q & 7) * wstep, 0, 0);
     else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)d, 16, (q & 1) ? xoff1 : xoff0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.rx, (lds_void*)d, 16, (q & 1) ? r.xoff1 : r.xoff0,
                                                k * 2 + (q & 7) * xstep, 0, 0);
   }
+  __device__ __forceinline__ void issue(int stage, int k, int q) { issue(src, stage, k, q); }
 
   // Fragment f (0..7: weight blocks, 8..15: x blocks) of K half h of a stage.
   __device__ __forceinline__ void read(int buf, int stage, int h, int f) {
@@ -663,8 +714,12 @@ struct W4Tile {
     for (int j = 1; j < n; ++j) stage(j, std::false_type{});
     w4_wait<0, 0>();
     w4_barrier();
-    // The MFMA results are read below: 32 wait states, in statements that
-    // take every accumulator, so no read moves above them.
+    fence_results();
+  }
+
+  // The MFMA results are read next: 32 wait states, in statements that take
+  // every accumulator, so no read moves above them.
+  __device__ __forceinline__ void fence_results() {
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
       if (a == 0)
@@ -743,40 +798,10 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm_w4_kernel(GemmArgs g) {
   tile_origin(g, t, NB == 1 ? kBW : kBW / 2, m0, n0);
 
   W4Tile<NB> c;
-  c.lds = (lds_char*)smem;
-  const int lane = threadIdx.x & 63;
-  c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  c.wm = c.wave & 1;
-  c.wn = c.wave >> 1;
-  c.frow = lane & 15;
-  c.fch = lane >> 4;
-  // the tile owns x rows [m0, mlim); x rows past it read as zero
+  c.init(smem, g);
+  // the tile owns x rows [m0, mlim)
   const int64_t mlim = std::min<int64_t>(g.M, (int64_t)m0 + g.bm);
-  const bool up = NB == 2 && c.wave >= 2;
-  const uint16_t* wsrc = up ? g.w1 : g.w0;
-  const int64_t ldw = up ? g.ldw1 : g.ldw0;
-  const int wrow0 = NB == 1 ? n0 + c.wave * 64 : n0 + (c.wave & 1) * 64;
-  c.rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(mlim * g.ldx * 2),
-                                           0x00020000);
-  c.rw = __builtin_amdgcn_make_buffer_rsrc((void*)wsrc, (short)0, (int)(g.N * ldw * 2),
-                                           0x00020000);
-  // staged row wave*64 + q*8 + lr: its swizzle depends on lr and q's parity
-  const int lr = lane >> 3, lc = lane & 7;
-  const int c0 = (lc ^ w4_swz(lr)) * 16, c1 = (lc ^ w4_swz(8 + lr)) * 16;
-  const int xoff = (int)((int64_t)(m0 + c.wave * 64 + lr) * g.ldx * 2);
-  const int woff = (int)((int64_t)(wrow0 + lr) * ldw * 2);
-  c.xoff0 = xoff + c0;
-  c.xoff1 = xoff + c1;
-  c.woff0 = woff + c0;
-  c.woff1 = woff + c1;
-  c.xstep = __builtin_amdgcn_readfirstlane((int)(8 * g.ldx * 2));
-  c.wstep = __builtin_amdgcn_readfirstlane((int)(8 * ldw * 2));
-  // a fragment's 16 rows start at a multiple of 16: the swizzle of its
-  // rows depends on the lane only
-  c.fo0 = c.frow * kW4Row + ((c.fch ^ w4_swz(c.frow)) * 16);
-  c.fo1 = c.frow * kW4Row + (((4 + c.fch) ^ w4_swz(c.frow)) * 16);
-  // x fragments: wave pair wm takes rows [wm * 128, ...) of the tile
-  c.xbase = c.wm * 128;
+  c.src = c.bind(g, m0, n0, mlim);
   const int live = (int)(mlim - m0) - c.xbase;
   const int nbx = __builtin_amdgcn_readfirstlane(live <= 0 ? 0 : min(8, (live + 15) / 16));
   const int n = (int)(g.K / kW4BK);
