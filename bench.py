@@ -11,10 +11,11 @@ the BASELINE shapes, every kernel launched once through the C ABI:
   rope_vision      q, k [16384,16,80] views of packed qkv, fp32 cos/sin (config 4)
   q_proj, o_proj   [3100,4096] x [4096,4096]^T      (config 3)
   gate_silu_mul    [3100,4096] x 2 x [12288,4096]^T (config 3, P5)
-  down_proj        [3100,12288] x [4096,12288]^T on this library's stream-K
-                   linear, which the fused MLP uses for this shape (the
-                   reference keeps the vendor BLAS); with P5 it makes the LM
-                   MLP prefill.
+  down_proj        [3100,12288] x [4096,12288]^T on this library's linear
+                   (208 output tiles: the data-parallel four-wave kernel),
+                   which the fused MLP uses for this shape (the reference
+                   keeps the vendor BLAS); with P5 it makes the LM MLP
+                   prefill.
   down_proj_vendor the same GEMM on the vendor BLAS (F.linear, hipBLASLt),
                    measured beside it for that per-site choice.
 
@@ -451,8 +452,9 @@ def load_traffic(name: str):
 
 
 # kernel-name fragment of each bench entry whose traffic can be measured live
-TRAFFIC_KERNELS = {"gate_silu_mul": "gemm_kernel<2,", "q_proj/o_proj": "gemm_kernel<1,",
-                   "down_proj": "gemm_sk_kernel<"}
+# (a probe launches one entry only, so q/o and down_proj may share a kernel)
+TRAFFIC_KERNELS = {"gate_silu_mul": "gemm_w4_kernel<2,", "q_proj/o_proj": "gemm_w4_kernel<1,",
+                   "down_proj": "gemm_w4_kernel<1,"}
 COPY_KERNEL = "__amd_rocclr_copyBuffer"  # the HIP runtime's device copy (the probe's calibration)
 
 

@@ -239,9 +239,11 @@ int umic_linear_bf16(const void* x, const void* w, const void* bias, void* out,
 
 /*
  * Bytes of device workspace umic_linear_ws_bf16 uses for this shape on the
- * current device: nonzero when the output has fewer 256 x 256 tiles than
- * the device has CUs (then a stream-K schedule spreads the K loop over every
- * CU), 0 when the data-parallel kernel is used and no workspace is needed.
+ * current device: nonzero when the output's 256 x 256 tiles leave enough of
+ * the device's CUs idle and the K loop is long (then a stream-K schedule
+ * spreads the K loop over every CU; with K % 64 == 0, at most 11/16 of the
+ * CUs' count in tiles, as the data-parallel kernel is faster beyond), 0 when
+ * the data-parallel kernel is used and no workspace is needed.
  * Host-only query; enqueues nothing.
  */
 int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
@@ -277,9 +279,10 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
  * those, as there.  A shape whose stream-K workspace
  * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 85 output tiles
  * of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  At N = 4096,
- * K = 12288 (the MLP down projection) that admits M <= 1280; the BASELINE
- * prefill (M = 3100, 208 tiles, 156 MiB) does not fit and needs
- * umic_linear_ws_bf16.  The device's first call clears the scratch's
+ * K = 12288 (the MLP down projection) that admits M <= 1280; M from 1281
+ * to 2816 (stream-K, over 64 MiB) needs umic_linear_ws_bf16, and the
+ * BASELINE prefill (M = 3100, 208 tiles) runs the data-parallel kernel
+ * here too.  The device's first call clears the scratch's
  * counter region with a kernel (no memset); every launch leaves it cleared.
  * All calls on one device share its scratch: calls that may overlap in time
  * on one device (different streams without ordering) may give wrong

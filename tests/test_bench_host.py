@@ -12,7 +12,7 @@ import pytest
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 import bench  # noqa: E402
 
-P5 = "void umic::(anonymous namespace)::gemm_kernel<2, 0, false>(umic::GemmArgs)"
+P5 = "void umic::(anonymous namespace)::gemm_w4_kernel<2, 0, false>(umic::GemmArgs)"
 COPY = "__amd_rocclr_copyBuffer"
 
 
@@ -22,14 +22,14 @@ def rows(*pairs):
 
 def test_copy_and_kernel_take_the_last_dispatch_of_each():
     r = rows(("void at::native::fill_kernel", 5.0), (COPY, 100.0), (COPY, 262144.0),
-             (P5, 1.0), ("void umic::gemm_kernel<1, 0, false>", 7.0), (P5, 599641.875))
+             (P5, 1.0), ("void umic::gemm_w4_kernel<1, 0, false>", 7.0), (P5, 599641.875))
     assert bench.pmc_copy_and_kernel(r, bench.TRAFFIC_KERNELS["gate_silu_mul"]) == \
         (262144.0, 599641.875)
 
 
 @pytest.mark.parametrize("r", [rows((P5, 1.0)), rows((COPY, 2.0)), rows((COPY, 0.0), (P5, 1.0))])
 def test_missing_or_empty_calibration_is_reported(r):
-    assert bench.pmc_copy_and_kernel(r, "gemm_kernel<2,") is None
+    assert bench.pmc_copy_and_kernel(r, "gemm_w4_kernel<2,") is None
 
 
 def test_counters_are_scaled_by_the_copy():

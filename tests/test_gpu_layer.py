@@ -3,7 +3,7 @@ injection (hidden 4096, 32 q / 8 kv heads, head_dim 128,
 intermediate 12288, random N(0, 0.02) weights, norms 1 + N(0, 0.1)).
 
 Prefill (M=3100) takes every fused kernel whose site wins there (P5, the
-stream-K down_proj, norms, RoPE; q/o_proj stay on hipBLASLt) -- checked by
+tiled down_proj, norms, RoPE; q/o_proj stay on hipBLASLt) -- checked by
 counting the C-ABI calls -- and decode (M=1) takes the library's GEMV for the
 GEMM sites while norms and RoPE stay fused.  Outputs are compared with the
 unpatched layer on the same GPU within the GEMM tolerance.
@@ -73,8 +73,9 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
         assert call_log["umic_linear_add_bf16"] == 1
         assert call_log["umic_linear_ws_bf16"] + call_log["umic_linear_bf16"] == 2
     else:
-        # the MLP's down_proj on the stream-K linear; q/o_proj stay on
-        # hipBLASLt, faster than the tiled linear at this shape
+        # the MLP's down_proj on the tiled linear (in its row band); q/o_proj
+        # stay on hipBLASLt, which the tiled linear only ties at this shape
+        assert integrate.TILED_MIN_ROWS_DOWN <= M <= integrate.TILED_MAX_ROWS_DOWN
         assert integrate.TILED_MIN_ROWS_LINEAR is None
         assert call_log["umic_linear_add_bf16"] == 0
         assert call_log["umic_linear_ws_bf16"] == 1 and call_log["umic_linear_bf16"] == 0

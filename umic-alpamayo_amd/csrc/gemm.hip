@@ -1337,9 +1337,15 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
 // reduction's device-scope loads, extra prologues), measured on MI355X, so
 // the main segment must be at least kSkMinMain steps (q/o at K = 4096 stays
 // data-parallel; down_proj at K = 12288 gains ~10%); every tail workgroup
-// keeps at least kSkMinSteps steps.
+// keeps at least kSkMinSteps steps.  Stream-K runs on the eight-wave core,
+// the data-parallel kernel on the faster four-wave core (K % 64 == 0), so a
+// shape whose tiles already fill most CUs stays data-parallel: at N = 4096,
+// K = 12288 (MI355X, 256 CUs, us data-parallel / stream-K) M = 512 (32
+// tiles): 263 / 169, 2048 (128): 270 / 219, 2560 (160): 274 / 250, 2816
+// (176): 279 / 267, 3100 (208): 252 / 269 -- stream-K up to 11/16 of the CUs.
 constexpr int kSkMinSteps = 16;
 constexpr int kSkMinMain = 192;
+constexpr int kSkMaxTileShare16 = 11;  // tiles <= CUs * 11 / 16
 
 struct SkPlan {
   int64_t tiles;
@@ -1362,6 +1368,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   const int64_t G = std::min<int64_t>(cus, 2 * T - 1);
   if (cus <= 0 || G <= T || T * KT * G >= ((int64_t)1 << 31)) return pl;
   if (T > kSkMaxTiles) return pl;
+  if (K % kW4BK == 0 && T * 16 > cus * kSkMaxTileShare16) return pl;
   // Main workgroups take a sixth of the tail beyond the even share, which
   // offsets the tail workgroups' extra segment prologues and partial stores
   // and makes a main workgroup usually the last to arrive at its tile.

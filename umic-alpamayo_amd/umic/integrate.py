@@ -78,26 +78,31 @@ GEMV_ROWS_DOWN = 2    # the MLP's down projection (and its residual epilogue)
 
 
 # The tiled MFMA kernels against the vendor path they replace, per site and
-# row count (config-5 and ViT shapes, one MI355X, every launch in a HIP graph
-# over rotating operands; fused time / vendor time):
+# row count (config-5 and ViT shapes, one MI355X, each site's launches
+# captured in one HIP graph over rotating operand sets, >= 640 MB a turn;
+# fused time / vendor time):
 #   P5 gate/up + SiLU*mul (K = 4096, N = 2 x 12288) vs two GEMMs, silu, mul:
-#     M = 64: 1.48, 256: 0.93, 512: 0.85, 1024: 1.02, 2048: 0.89, 3100: 0.90, 4096: 0.99
+#     M = 64: 1.45, 256: 0.91, 512: 0.82, 1024: 0.88, 2048: 0.78, 3100: 0.82, 4096: 0.91
 #   ViT fc1 + bias + tanh GELU (K = 1280, N = 5120) vs F.linear then F.gelu:
-#     M = 64: 2.7, 256: 1.9, 1024: 1.39, 2048: 0.95, 4096: 1.04, 8192: 0.87, 16384: 1.02
-#   down_proj on the stream-K linear (K = 12288, N = 4096):
-#     M = 64: 4.3, 512: 2.0, 1024: 1.47, 2048: 1.24, 3100: 1.00
+#     M = 256: 1.86, 1024: 1.36, 2048: 0.98, 4096: 1.00, 8192: 0.90, 16384: 0.91
+#   down_proj linear (K = 12288, N = 4096; stream-K up to 2816 rows):
+#     M = 64: 3.71, 512: 2.01, 1024: 1.46, 2048: 1.16, 2816: 1.17, 2900: 1.12,
+#     3000: 1.17, 3100: 0.88, 3300: 0.98, 3500: 1.03, 3800: 1.03, 4096: 1.07
 #   plain q/o_proj linear (K = N = 4096):
-#     M = 64: 4.2, 256: 3.5, 1024: 2.1, 2048: 1.52, 3100: 1.17, 4096: 1.23
+#     M = 64: 5.1, 256: 4.1, 1024: 2.05, 2048: 1.37, 2900: 1.06, 3000: 1.07,
+#     3100: 1.00, 3300: 1.04, 3500: 1.05, 3800: 0.98, 4096: 1.10, 8192: 1.10
 # The 256 x 256 tiles leave most CUs idle below a few thousand rows, where
-# hipBLASLt picks smaller tiles.  So each site takes its tiled kernel only
-# from the row count where it stops losing (the reference's own rule: fuse a
-# site only where measured faster, integrate.py:80-91): P5 from 256 rows,
-# fc1 + GELU from 2048, the stream-K down_proj from 3072; the plain q/o
-# linear never (None), hipBLASLt being faster at every measured row count.
-# The decode GEMV regime above is separate.
+# hipBLASLt picks smaller tiles; from there both run at the chip's power
+# cap and the vendor's kernel choice decides.  So each site takes its tiled
+# kernel only where it stops losing (the reference's own rule: fuse a site
+# only where measured faster, integrate.py:80-91): P5 from 256 rows, fc1 +
+# GELU from 2048, down_proj in the 13-tile-row band 3072..3328 (where
+# hipBLASLt's pick is slow); the plain q/o linear never (None): a tie at
+# 3100 rows and one 2% win at 3800 among 4-10% losses.
 TILED_MIN_ROWS_MLP = 256
 TILED_MIN_ROWS_GELU_MLP = 2048
 TILED_MIN_ROWS_DOWN = 3072
+TILED_MAX_ROWS_DOWN = 3328
 TILED_MIN_ROWS_LINEAR: int | None = None
 
 
@@ -135,12 +140,10 @@ INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
 
 # Per-site choice for the P5 MLP's down_proj, which the reference leaves on
 # the vendor BLAS (integrate.py:80-90, measured a loser on Thor): on MI355X
-# this library's stream-K linear ties or beats hipBLASLt where it applies
-# (fewer output tiles than CUs and a long K loop) from TILED_MIN_ROWS_DOWN
-# rows (at M=3100, K=12288: 283 vs 283 us graph-timed, 286 vs 310 us in
-# bench.py's back-to-back timing), so the fused MLP uses it for exactly those
-# shapes and the vendor module for every other one.
-DOWN_PROJ_STREAM_K = True
+# this library's linear beats hipBLASLt in the TILED_MIN_ROWS_DOWN ..
+# TILED_MAX_ROWS_DOWN band (M = 3100: 257 vs 291 us graph-timed), so the
+# fused MLP uses it there and the vendor module for every other row count.
+DOWN_PROJ_TILED = True
 
 # ViT projection site list kept from the reference (integrate.py:95); not
 # used by apply().
@@ -190,9 +193,9 @@ def _fused_mlp_forward(self: nn.Module, x: torch.Tensor) -> torch.Tensor:
     down = self.down_proj
     if _rows(h) < FUSE_MIN_ROWS:
         return _linear(down, h, GEMV_ROWS_DOWN)
-    if (DOWN_PROJ_STREAM_K and isinstance(down, nn.Linear) and _rows(h) >= TILED_MIN_ROWS_DOWN
-            and linear.linear_eligible(h, down.weight, down.bias)
-            and linear.stream_k_planned(h, down.weight)):
+    if (DOWN_PROJ_TILED and isinstance(down, nn.Linear)
+            and TILED_MIN_ROWS_DOWN <= _rows(h) <= TILED_MAX_ROWS_DOWN
+            and linear.linear_eligible(h, down.weight, down.bias)):
         return linear.linear_hip(h, down.weight, down.bias)
     return down(h)
 
