@@ -344,6 +344,52 @@ int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void* wu,
                             int64_t ldx, int64_t ldwg, int64_t ldwu,
                             int64_t ldo, void* stream);
 
+/*
+ * Decode-step RMSNorm fused into the q/k/v multi-linear GEMV:
+ *   y = RMSNorm(x) with norm_w and eps (umic_rmsnorm_bf16's numerics on the
+ *   M x K rows), then out_i = y @ w_i^T + bias_i as umic_linear_multi_bf16
+ *   (act none) -- one launch, no trip of y through memory: every workgroup
+ *   normalizes the rows itself from L2 while its first weight loads are in
+ *   flight.  Results are bit-identical to umic_rmsnorm_bf16 followed by
+ *   umic_linear_multi_bf16.  normed: optional [M, >= ldn] copy of y (NULL:
+ *   not written; written only when some N_i > 0), which must not overlap x.
+ *   Requires 1 <= M <= 2 and a row length K whose eager reduction plan is
+ *   the single-block one without a row split and at most four 4-vectors
+ *   per thread (with K % 32 == 0: every K from 512 to 4096), 8-byte
+ *   aligned norm_w and normed (ldn % 4 == 0), plus umic_linear_multi_bf16's
+ *   rules; else UMIC_ERR_UNSUPPORTED.
+ * No single counterpart in the reference: replaces the decoder layer's
+ * input_layernorm forward (integrate.py:134-141 on Qwen3VLTextRMSNorm)
+ * followed by the q/k/v projections (integrate.py:91, 98-107; in the
+ * reference three linear launches) at the decode steps.
+ */
+int umic_rmsnorm_linear_multi_bf16(const void* x, const void* norm_w, void* normed,
+                                   int64_t M, int64_t K, int64_t ldx, int64_t ldn,
+                                   float eps, int count, const void* const* w,
+                                   const void* const* bias, void* const* out,
+                                   const int64_t* N, const int64_t* ldw, const int64_t* ldo,
+                                   void* stream);
+
+/*
+ * Decode-step residual add + RMSNorm fused into the P5 GEMV:
+ *   summed = bf16(x + r); normed = RMSNorm(summed) (umic_add_rmsnorm_bf16's
+ *   numerics); out = silu(normed @ wg^T) * (normed @ wu^T) as
+ *   umic_gate_silu_mul_bf16 -- one launch.  Bit-identical to
+ *   umic_add_rmsnorm_bf16 followed by umic_gate_silu_mul_bf16.  normed and
+ *   summed are optional outputs (NULL: not written) that must not overlap x
+ *   or r.  Same row rules as umic_rmsnorm_linear_multi_bf16 (r 8-byte
+ *   aligned, ldr % 4 == 0), plus umic_gate_silu_mul_bf16's.
+ * No single counterpart in the reference: replaces the decoder layer's
+ * residual add and post_attention_layernorm forward followed by
+ * kernels/fused_ffn.py:93-118 (gate_silu_mul_triton) at the decode steps.
+ */
+int umic_add_rmsnorm_gate_silu_mul_bf16(const void* x, const void* r, const void* norm_w,
+                                        void* normed, void* summed, const void* wg,
+                                        const void* wu, void* out, int64_t M, int64_t N,
+                                        int64_t K, int64_t ldx, int64_t ldr, int64_t ldn,
+                                        int64_t lds, int64_t ldwg, int64_t ldwu, int64_t ldo,
+                                        float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,10 +63,16 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
           flush=True)
     assert e1 <= TOL and e2 <= TOL
     assert call_log["umic_rmsnorm_bf16"] == 3          # input_layernorm, q_norm, k_norm
-    assert call_log["umic_add_rmsnorm_bf16"] == 1
     assert call_log["umic_rope_qk_bf16"] == 1          # q and k in one launch
-    # P5 tiled at prefill, the GEMV at decode (one row)
-    assert call_log["umic_gate_silu_mul_bf16"] == 1
+    if M == 1:
+        # the post-attention residual add + RMSNorm folded into the P5 GEMV
+        assert call_log["umic_add_rmsnorm_gate_silu_mul_bf16"] == 1
+        assert call_log["umic_add_rmsnorm_bf16"] == 0
+        assert call_log["umic_gate_silu_mul_bf16"] == 0
+    else:
+        # P5 on the tiled kernel after the fused add + RMSNorm
+        assert call_log["umic_add_rmsnorm_bf16"] == 1
+        assert call_log["umic_gate_silu_mul_bf16"] == 1
     if M == 1:
         # q_proj and o_proj on the GEMV; the down projection carries the MLP
         # residual add in its epilogue

@@ -505,3 +505,26 @@ def test_kernel_registry():
         assert kernels.get_kernel("rmsnorm") is mine
     finally:
         kernels.register_kernel("rmsnorm", rmsnorm.rmsnorm_hip)
+
+
+def test_gemv_norm_plan_matches_torch_reduce_config():
+    """The folded-norm plan restates Reduce.cuh's setReduceConfig: at one row
+    and n = 4096, 512 threads with two 4-vectors each; two rows split the
+    block, 256 threads with four; short rows (< 128 threads) and long rows
+    (16+ values per thread: the row would be split over the block) are not
+    the wide plan."""
+    from umic.kernels import rmsnorm
+
+    assert rmsnorm.wide_plan(1, 4096) == (512, 2)
+    assert rmsnorm.wide_plan(2, 4096) == (256, 4)
+    assert rmsnorm.wide_plan(1, 2048) == (512, 1)
+    assert rmsnorm.wide_plan(1, 7680) == (512, 4)
+    assert rmsnorm.wide_plan(2, 7936) == (256, 8)
+    assert rmsnorm.wide_plan(4, 4096) == (128, 8)
+    for rows, n in ((1, 256), (1, 504), (1, 8192), (2, 8192), (1, 7688), (1, 100)):
+        assert rmsnorm.wide_plan(rows, n) is None, (rows, n)
+    assert rmsnorm.gemv_norm_ok(1, 4096) and rmsnorm.gemv_norm_ok(2, 512)
+    assert rmsnorm.gemv_norm_ok(2, 4096) and rmsnorm.gemv_norm_ok(1, 3072)
+    # past four vectors per thread (k4 = 3 at 512 threads), more rows, odd n
+    assert not rmsnorm.gemv_norm_ok(1, 4608) and not rmsnorm.gemv_norm_ok(1, 7680)
+    assert not rmsnorm.gemv_norm_ok(3, 4096) and not rmsnorm.gemv_norm_ok(1, 4100)

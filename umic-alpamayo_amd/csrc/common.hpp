@@ -54,6 +54,19 @@ __device__ __forceinline__ void rbf2(float& a, float& b) {
   b = bf_hi(w);
 }
 
+// 4 bf16 values <-> 4 floats
+__device__ __forceinline__ void unpack4(const u32x2& v, float f[4]) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+}
+
+__device__ __forceinline__ u32x2 pack4(const float f[4]) {
+  u32x2 v;
+  v.x = pack2(f[0], f[1]);
+  v.y = pack2(f[2], f[3]);
+  return v;
+}
+
 // 8 bf16 values <-> 8 floats
 __device__ __forceinline__ void unpack8(const u32x4& v, float f[8]) {
   f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
@@ -174,9 +187,50 @@ __device__ __forceinline__ float rsqrt_cr(float v) {
   return tiny ? r * 0x1p32f : r;
 }
 
+// ---- torch's reduction plan for the RMSNorm statistic (host side) --------
+
+// setReduceConfig (Reduce.cuh) for a contiguous fp32 [rows, n] tensor reduced
+// over its last dim on a 64-lane, 512-threads-per-block device: vec = the
+// threads read 4-element vectors (n >= 128), bw threads across a row, bh the
+// block height, split = the row is also divided over the bh wavefronts.
+struct RmsPlan {
+  int vec, bw, bh, split;
+};
+
+inline int last_pow2(int64_t v) {
+  int p = 1;
+  while ((int64_t)p * 2 <= v) p *= 2;
+  return p;
+}
+
+// false when torch would also split rows across blocks (n >= 131072)
+inline bool rms_plan(int64_t rows, int64_t n, RmsPlan& p) {
+  constexpr int kMaxThreads = 512;
+  int64_t dim0 = n;
+  p.vec = dim0 >= 128;
+  if (p.vec) dim0 /= 4;
+  const int d0 = dim0 < kMaxThreads ? last_pow2(dim0) : kMaxThreads;
+  const int d1 = rows < kMaxThreads ? last_pow2(rows) : kMaxThreads;
+  int bw = d0 < kWave ? d0 : kWave;
+  const int bh = d1 < kMaxThreads / bw ? d1 : kMaxThreads / bw;
+  bw = d0 < kMaxThreads / bh ? d0 : kMaxThreads / bh;
+  const int64_t vpt = (n + bw - 1) / bw;
+  p.bw = bw;
+  p.bh = bh;
+  p.split = vpt >= (bh * 16 < 256 ? bh * 16 : 256);
+  return !(p.split && (n + (int64_t)bw * bh - 1) / ((int64_t)bw * bh) >= 256);
+}
+
 // ---- host-side argument checks -------------------------------------------
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+
+// Byte ranges [a, a + na) and [b, b + nb) share a byte.
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return na > 0 && nb > 0 && x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+}
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -1122,6 +1122,20 @@ struct GemvSeg {
   uint16_t* out;
   int64_t N, ldw0, ldw1, ldo;
 };
+// The RMSNorm (optionally after a residual add) that a norm-prologue launch
+// applies to x before the GEMV: y = bf16(w * bf16(v * rstd)), v = x or
+// bf16(x + r), rstd from the sum of v^2 in the order of torch's wide
+// reduction plan (bw reducing threads, k4 4-vectors each, norm.hip's
+// rms_wide_kernel).  Workgroup 0 writes v (s, ADD) and y when asked.
+struct GemvNorm {
+  const uint16_t* w;  // [K] norm weight
+  const uint16_t* r;  // residual rows (add form)
+  uint16_t* s;        // bf16(x + r) rows out (add form), or NULL
+  uint16_t* y;        // normalized rows out, or NULL
+  int64_t ldr, lds, ldy;
+  float factor, eps;
+  int bw, k4;
+};
 struct GemvJob {
   const uint16_t* x;
   const uint16_t* resid;  // out = bf16(resid + bf16(result)), or NULL
@@ -1129,7 +1143,13 @@ struct GemvJob {
   GemvSeg seg[kGemvMaxSegs];
   int64_t first[kGemvMaxSegs + 1];
   int count;
+  GemvNorm nrm;  // used by the norm-prologue instantiations only
 };
+
+// Rows and LDS of the norm-prologue launches: each workgroup keeps the
+// normalized rows (MR x K bf16) in LDS.
+constexpr int kGemvNormMaxRows = 2;
+constexpr int64_t kGemvNormMaxLds = 64 << 10;
 
 // FULL: K is a whole number of passes (every slab of every pass is inside
 // K: K a multiple of 2048 U, as 4096 and 12288), so the per-slab bounds
@@ -1307,6 +1327,281 @@ int device_cus() {
     cus[dev] = n;
   }
   return cus[dev];
+}
+
+// ---- Norm-folded GEMV (decode) --------------------------------------------
+//
+// The decode GEMV with the RMSNorm of its input (after a residual add, ADD)
+// folded in.  The norm's statistic spans the whole row, so every workgroup
+// computes it itself, from L2, once: the launch is persistent (a grid that
+// fits on the device at once), and each workgroup normalizes the MR rows into
+// LDS, then walks the column groups blockIdx.x, + gridDim.x, ...  The norm's
+// loads are issued before the first group's weight loads (a wait for them
+// then does not wait for the weights), kept in registers, and the
+// normalization is exactly rms_wide_kernel<ADD, bw, k4>'s (norm.hip): thread
+// t plays reducing threads t and t + 256, each summing the squares of its
+// 4-vectors vt, vt + bw, ... into four accumulators, ((a0 + a1) + a2) + a3,
+// wavefront 0 halving the bw / 64 wavefront columns and finishing with the
+// in-wavefront tree, the correctly rounded rsqrt, then bf16(w * bf16(v *
+// rstd)) in pairs.  The products, their order and the epilogue are
+// gemv_kernel's (act none, optional bias), so results are bit-identical to
+// the RMSNorm launch followed by the GEMV launch.
+constexpr int kNormPV = 4;  // 4-vectors per thread and row
+
+template <int NB, bool BIAS, int MR, bool FULL, bool ADD>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_norm_kernel(GemvJob job) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [MR][K] normalized rows
+  __shared__ float red[512];
+  __shared__ float stat[MR];
+  constexpr int R = kGemvCols;
+  constexpr int U = 2;
+  __shared__ float part[kGemvWaves][MR * NB * R];
+  const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t K = job.K, chunks = K / 8;
+  const int64_t total = job.first[job.count];
+  const GemvNorm& nm = job.nrm;
+  const int bw = nm.bw, k4 = nm.k4, nv = (int)(K / 4);
+  const int nvt = bw > 256 ? 2 : (t < bw ? 1 : 0);  // reducing threads played by t
+  // 1. the norm's operands of this thread: vector j is reducing thread
+  //    t + (j / k4) * 256's k = j % k4 th
+  int pidx[kNormPV];
+  bool pok[kNormPV];
+  u32x2 px[MR][kNormPV], pw[kNormPV];
+  [[maybe_unused]] u32x2 pr[MR][kNormPV];
+#pragma unroll
+  for (int j = 0; j < kNormPV; ++j) {
+    const int a = j / k4, k = j - a * k4;
+    const int idx = t + a * 256 + k * bw;
+    pok[j] = a < nvt && idx < nv;
+    pidx[j] = pok[j] ? idx : 0;
+    if (pok[j]) {
+      pw[j] = *reinterpret_cast<const u32x2*>(nm.w + pidx[j] * 4);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        px[m][j] = *reinterpret_cast<const u32x2*>(job.x + m * job.ldx + pidx[j] * 4);
+        if constexpr (ADD) pr[m][j] = *reinterpret_cast<const u32x2*>(nm.r + m * nm.ldr + pidx[j] * 4);
+      }
+    }
+  }
+  // 2. the first group's weights
+  int64_t blk = blockIdx.x;
+  const uint16_t* wr[NB][R];
+  int64_t n0 = 0;
+  int si = 0;
+  auto setup = [&](int64_t b) {
+    si = 0;
+#pragma unroll
+    for (int i = 1; i < kGemvMaxSegs; ++i)
+      if (i < job.count && b >= job.first[i]) si = i;
+    const GemvSeg& sg = job.seg[si];
+    n0 = (b - job.first[si]) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = n0 + r < sg.N ? n0 + r : sg.N - 1;
+      wr[0][r] = sg.w0 + n * sg.ldw0;
+      if constexpr (NB == 2) wr[NB - 1][r] = sg.w1 + n * sg.ldw1;
+    }
+  };
+  u32x4 wv[U][NB][R];
+  auto load_w = [&](int64_t cb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = FULL || cb + 64 * u < chunks ? cb + 64 * u : cb;  // cb < chunks
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          wv[u][b][r] = ld_stream(reinterpret_cast<const u32x4*>(wr[b][r] + c * 8));
+    }
+  };
+  const int64_t c0 = lane + (int64_t)64 * U * wave;
+  setup(blk);
+  if (c0 < chunks) load_w(c0);
+  // 3. the norm, row by row, into xs
+  const bool lead = blockIdx.x == 0;
+  auto vals = [&](int m, int j, float f[4]) {
+    unpack4(px[m][j], f);
+    if constexpr (ADD) {
+      float rf[4];
+      unpack4(pr[m][j], rf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] = rbf(f[e] + rf[e]);
+    }
+  };
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kNormPV; ++j) {
+        if (j / k4 != a || !pok[j]) continue;
+        float f[4];
+        vals(m, j, f);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = acc[i] + f[i] * f[i];
+      }
+      if (a < nvt) red[t + a * 256] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    }
+    __syncthreads();
+    if (t < kWave) {
+      for (int h = bw / kWave / 2; h >= 1; h >>= 1)
+        for (int w = 0; w < h; ++w)
+          red[w * kWave + lane] = red[w * kWave + lane] + red[(w + h) * kWave + lane];
+      const float tot = group_sum<kWave>(red[lane]);
+      if (t == 0) stat[m] = rsqrt_cr(tot * nm.factor + nm.eps);
+    }
+    __syncthreads();
+    const float rstd = stat[m];
+#pragma unroll
+    for (int j = 0; j < kNormPV; ++j) {
+      if (!pok[j]) continue;
+      float f[4], wf[4], o[4];
+      vals(m, j, f);
+      if (ADD && lead && nm.s) *reinterpret_cast<u32x2*>(nm.s + m * nm.lds + pidx[j] * 4) = pack4(f);
+      unpack4(pw[j], wf);
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {  // bf16(v * rstd) in pairs
+        float p0 = f[e] * rstd, p1 = f[e + 1] * rstd;
+        rbf2(p0, p1);
+        o[e] = wf[e] * p0;
+        o[e + 1] = wf[e + 1] * p1;
+      }
+      const u32x2 y = pack4(o);
+      *reinterpret_cast<u32x2*>(xs + m * K + pidx[j] * 4) = y;
+      if (lead && nm.y) *reinterpret_cast<u32x2*>(nm.y + m * nm.ldy + pidx[j] * 4) = y;
+    }
+  }
+  __syncthreads();
+  // 4. the column groups: gemv_kernel's products and epilogue on xs.  A
+  //    group's first-pass weights were loaded before it starts (the next
+  //    group's go out right after this group's products, so they are in
+  //    flight through its reduction and stores).
+  while (true) {
+    const int cur_si = si;
+    const int64_t cur_n0 = n0;
+    float acc[MR][NB][R];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][b][r] = 0.0f;
+    for (int64_t cb = c0; cb < chunks; cb += 64 * U * kGemvWaves) {
+      if (cb != c0) load_w(cb);
+      u32x4 xv[U][MR];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = FULL || cb + 64 * u < chunks ? cb + 64 * u : cb;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) xv[u][m] = *reinterpret_cast<const u32x4*>(xs + m * K + c * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!FULL && cb + 64 * u >= chunks) break;
+        float xf[MR][8];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) unpack8(xv[u][m], xf[m]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float wf[8];
+            unpack8(wv[u][b][r], wf);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc[m][b][r] = __builtin_fmaf(wf[e], xf[m][e], acc[m][b][r]);
+          }
+      }
+    }
+    const int64_t next = blk + gridDim.x;
+    if (next < total) {
+      setup(next);
+      if (c0 < chunks) load_w(c0);
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int s = 32; s >= 1; s >>= 1) acc[m][b][r] += __shfl_xor(acc[m][b][r], s, kWave);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int r = 0; r < R; ++r) part[wave][(m * NB + b) * R + r] = acc[m][b][r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const GemvSeg& sg = job.seg[cur_si];
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float v = part[0][(m * NB + b) * R + r];
+#pragma unroll
+            for (int w = 1; w < kGemvWaves; ++w) v += part[w][(m * NB + b) * R + r];
+            acc[m][b][r] = v;
+          }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (lane != m) continue;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int64_t n = cur_n0 + r;
+          if (n >= sg.N) continue;
+          const float bias = BIAS && sg.bias ? bf2f(sg.bias[n]) : 0.0f;
+          const float o = gemv_epilogue<NB, UMIC_ACT_NONE, BIAS>(acc[m][0][r], acc[m][NB - 1][r], bias);
+          sg.out[m * sg.ldo + n] = (uint16_t)f2bf(o);
+        }
+      }
+    }
+    if (next >= total) break;
+    blk = next;
+    __syncthreads();  // part is refilled by the next group
+  }
+}
+
+// Workgroups of a persistent launch that fit on the device at once.
+template <typename Kern>
+int64_t resident_grid(Kern kern, size_t lds) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kGemvWaves * 64, lds) !=
+          hipSuccess || per_cu < 1)
+    per_cu = 1;
+  return (int64_t)device_cus() * per_cu;
+}
+
+template <int NB, bool BIAS, int MR, bool ADD>
+int launch_gemv_norm_mr(const GemvJob& job, hipStream_t st) {
+  const size_t lds = (size_t)(MR * job.K * 2);
+  const int64_t total = job.first[job.count];
+  if (job.K % 4096 == 0) {
+    auto kern = gemv_norm_kernel<NB, BIAS, MR, true, ADD>;
+    const int64_t grid = std::min<int64_t>(total, resident_grid(kern, lds));
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kGemvWaves * 64), lds, st, job);
+  } else {
+    auto kern = gemv_norm_kernel<NB, BIAS, MR, false, ADD>;
+    const int64_t grid = std::min<int64_t>(total, resident_grid(kern, lds));
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kGemvWaves * 64), lds, st, job);
+  }
+  return launch_status();
+}
+
+template <int NB, bool BIAS, bool ADD>
+int launch_gemv_norm(const GemvJob& job, hipStream_t st) {
+  const int64_t total = job.first[job.count];
+  if (total <= 0 || total > 0x7fffffffLL || device_cus() <= 0) return UMIC_ERR_UNSUPPORTED;
+  if (job.M == 1) return launch_gemv_norm_mr<NB, BIAS, 1, ADD>(job, st);
+  if (job.M == 2) return launch_gemv_norm_mr<NB, BIAS, 2, ADD>(job, st);
+  return UMIC_ERR_UNSUPPORTED;
 }
 
 template <int NB, int ACT, bool BIAS>
@@ -1589,27 +1884,17 @@ extern "C" int umic_gate_silu_mul_bf16(const void* x, const void* wg, const void
   return launch_gemm<2, UMIC_ACT_NONE, false>(g, as_stream(stream));
 }
 
-extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int count,
-                                      const void* const* w, const void* const* bias,
-                                      void* const* out, const int64_t* N, const int64_t* ldw,
-                                      const int64_t* ldo, int act, void* stream) {
-  if (M < 0 || K < 0 || count < 1 || count > kGemvMaxSegs) return UMIC_ERR_INVALID_ARG;
-  if (!w || !out || !N || !ldw || !ldo) return UMIC_ERR_INVALID_ARG;
-  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
-    return UMIC_ERR_INVALID_ARG;
-  for (int i = 0; i < count; ++i)
-    if (N[i] < 0) return UMIC_ERR_INVALID_ARG;
-  if (M == 0) return UMIC_OK;
-  if (M > kGemvMaxRows) return UMIC_ERR_UNSUPPORTED;
-  if (!x || ldx < K) return UMIC_ERR_INVALID_ARG;
-  if (K == 0) return UMIC_ERR_UNSUPPORTED;
-  GemvJob job{};
+// The segments of a multi-linear GEMV job, with umic_linear_multi_bf16's
+// argument checks; job.first[count] = 0 when every N is 0.
+int multi_job(GemvJob& job, const void* x, int64_t M, int64_t K, int64_t ldx, int count,
+              const void* const* w, const void* const* bias, void* const* out, const int64_t* N,
+              const int64_t* ldw, const int64_t* ldo, bool& any_bias) {
   job.x = (const uint16_t*)x;
   job.M = M;
   job.K = K;
   job.ldx = ldx;
   job.count = count;
-  bool any_bias = false;
+  any_bias = false;
   int64_t first = 0;
   for (int i = 0; i < count; ++i) {
     job.first[i] = first;
@@ -1625,7 +1910,28 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
     first += (N[i] + kGemvCols - 1) / kGemvCols;
   }
   job.first[count] = first;
-  if (first == 0) return UMIC_OK;
+  return UMIC_OK;
+}
+
+extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64_t ldx, int count,
+                                      const void* const* w, const void* const* bias,
+                                      void* const* out, const int64_t* N, const int64_t* ldw,
+                                      const int64_t* ldo, int act, void* stream) {
+  if (M < 0 || K < 0 || count < 1 || count > kGemvMaxSegs) return UMIC_ERR_INVALID_ARG;
+  if (!w || !out || !N || !ldw || !ldo) return UMIC_ERR_INVALID_ARG;
+  if (act != UMIC_ACT_NONE && act != UMIC_ACT_GELU && act != UMIC_ACT_GELU_TANH)
+    return UMIC_ERR_INVALID_ARG;
+  for (int i = 0; i < count; ++i)
+    if (N[i] < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0) return UMIC_OK;
+  if (M > kGemvMaxRows) return UMIC_ERR_UNSUPPORTED;
+  if (!x || ldx < K) return UMIC_ERR_INVALID_ARG;
+  if (K == 0) return UMIC_ERR_UNSUPPORTED;
+  GemvJob job{};
+  bool any_bias = false;
+  const int rc = multi_job(job, x, M, K, ldx, count, w, bias, out, N, ldw, ldo, any_bias);
+  if (rc != UMIC_OK) return rc;
+  if (job.first[count] == 0) return UMIC_OK;
   hipStream_t st = as_stream(stream);
   if (act == UMIC_ACT_GELU)
     return any_bias ? launch_gemv_job<1, UMIC_ACT_GELU, true>(job, st)
@@ -1635,6 +1941,92 @@ extern "C" int umic_linear_multi_bf16(const void* x, int64_t M, int64_t K, int64
                     : launch_gemv_job<1, UMIC_ACT_GELU_TANH, false>(job, st);
   return any_bias ? launch_gemv_job<1, UMIC_ACT_NONE, true>(job, st)
                   : launch_gemv_job<1, UMIC_ACT_NONE, false>(job, st);
+}
+
+// torch's reduction plan for an M x K RMSNorm when launch_rms (norm.hip)
+// runs it as the wide kernel, which the norm prologue reproduces; false for
+// any other plan, or rows / LDS beyond the prologue's limits.
+bool gemv_norm_plan(int64_t M, int64_t K, GemvNorm& nm) {
+  RmsPlan p;
+  if (M < 1 || M > kGemvNormMaxRows || K <= 0 || K % 8 || M * K * 2 > kGemvNormMaxLds)
+    return false;
+  if (!rms_plan(M, K, p) || !p.vec || p.split || p.bw < 128 || p.bw > 512) return false;
+  const int64_t k4 = (K / 4 + p.bw - 1) / p.bw;
+  if ((p.bw > 256 ? 2 : 1) * k4 > kNormPV) return false;  // the kernel's vectors per thread
+  nm.bw = p.bw;
+  nm.k4 = (int)k4;
+  nm.factor = (float)M / (float)(M * K);
+  return true;
+}
+
+// Bytes spanned by M rows of K bf16 at leading dim ld.
+inline int64_t row_span(int64_t M, int64_t K, int64_t ld) { return ((M - 1) * ld + K) * 2; }
+
+extern "C" int umic_rmsnorm_linear_multi_bf16(const void* x, const void* norm_w, void* normed,
+                                              int64_t M, int64_t K, int64_t ldx, int64_t ldn,
+                                              float eps, int count, const void* const* w,
+                                              const void* const* bias, void* const* out,
+                                              const int64_t* N, const int64_t* ldw,
+                                              const int64_t* ldo, void* stream) {
+  if (M < 0 || K < 0 || count < 1 || count > kGemvMaxSegs) return UMIC_ERR_INVALID_ARG;
+  if (!w || !out || !N || !ldw || !ldo) return UMIC_ERR_INVALID_ARG;
+  for (int i = 0; i < count; ++i)
+    if (N[i] < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0) return UMIC_OK;
+  if (!x || !norm_w || ldx < K || (normed && ldn < K)) return UMIC_ERR_INVALID_ARG;
+  if (K == 0) return UMIC_ERR_UNSUPPORTED;
+  GemvJob job{};
+  if (!gemv_norm_plan(M, K, job.nrm) || !aligned8(norm_w)) return UMIC_ERR_UNSUPPORTED;
+  if (normed && (!aligned8(normed) || ldn % 4)) return UMIC_ERR_UNSUPPORTED;
+  // every workgroup reads x while workgroup 0 writes normed
+  if (normed && overlaps(normed, row_span(M, K, ldn), x, row_span(M, K, ldx)))
+    return UMIC_ERR_INVALID_ARG;
+  bool any_bias = false;
+  const int rc = multi_job(job, x, M, K, ldx, count, w, bias, out, N, ldw, ldo, any_bias);
+  if (rc != UMIC_OK) return rc;
+  if (job.first[count] == 0) return UMIC_OK;
+  job.nrm.w = (const uint16_t*)norm_w;
+  job.nrm.y = (uint16_t*)normed;
+  job.nrm.ldy = ldn;
+  job.nrm.eps = eps;
+  hipStream_t st = as_stream(stream);
+  return any_bias ? launch_gemv_norm<1, true, false>(job, st)
+                  : launch_gemv_norm<1, false, false>(job, st);
+}
+
+extern "C" int umic_add_rmsnorm_gate_silu_mul_bf16(
+    const void* x, const void* r, const void* norm_w, void* normed, void* summed, const void* wg,
+    const void* wu, void* out, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldr,
+    int64_t ldn, int64_t lds, int64_t ldwg, int64_t ldwu, int64_t ldo, float eps, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return UMIC_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return UMIC_OK;  // empty tensors may carry null pointers
+  if (!x || !r || !norm_w || !wg || !wu || !out) return UMIC_ERR_INVALID_ARG;
+  if (ldx < K || ldr < K || ldwg < K || ldwu < K || ldo < N) return UMIC_ERR_INVALID_ARG;
+  if ((normed && ldn < K) || (summed && lds < K)) return UMIC_ERR_INVALID_ARG;
+  if (K == 0) return UMIC_ERR_UNSUPPORTED;
+  if (!gemm_shape_ok(x, wg, wu, out, M, N, K, ldx, ldwg, ldwu, ldo)) return UMIC_ERR_UNSUPPORTED;
+  GemmArgs g{(const uint16_t*)x, (const uint16_t*)wg, (const uint16_t*)wu, nullptr,
+             (uint16_t*)out, M, N, K, ldx, ldwg, ldwu, ldo, 0, 0};
+  GemvJob job = gemv_job(g);
+  if (!gemv_norm_plan(M, K, job.nrm) || !aligned8(norm_w) || !aligned8(r) || ldr % 4)
+    return UMIC_ERR_UNSUPPORTED;
+  if ((normed && (!aligned8(normed) || ldn % 4)) || (summed && (!aligned8(summed) || lds % 4)))
+    return UMIC_ERR_UNSUPPORTED;
+  // every workgroup reads x and r while workgroup 0 writes normed and summed
+  const int64_t sx = row_span(M, K, ldx), sr = row_span(M, K, ldr);
+  const int64_t sn = normed ? row_span(M, K, ldn) : 0, ss = summed ? row_span(M, K, lds) : 0;
+  if (overlaps(normed, sn, x, sx) || overlaps(normed, sn, r, sr) || overlaps(summed, ss, x, sx) ||
+      overlaps(summed, ss, r, sr))
+    return UMIC_ERR_INVALID_ARG;
+  job.nrm.w = (const uint16_t*)norm_w;
+  job.nrm.r = (const uint16_t*)r;
+  job.nrm.ldr = ldr;
+  job.nrm.s = (uint16_t*)summed;
+  job.nrm.lds = lds;
+  job.nrm.y = (uint16_t*)normed;
+  job.nrm.ldy = ldn;
+  job.nrm.eps = eps;
+  return launch_gemv_norm<2, false, true>(job, as_stream(stream));
 }
 
 extern "C" int umic_linear_add_bf16(const void* x, const void* w, const void* bias,

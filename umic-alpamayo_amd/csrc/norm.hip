@@ -66,41 +66,6 @@ struct NormArgs {
   float factor;  // RMSNorm: aten MeanOps factor, float(rows) / float(rows * n)
 };
 
-inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
-
-// ---- torch's reduction plan for the RMSNorm statistic (host side) --------
-
-// setReduceConfig (Reduce.cuh) for a contiguous fp32 [rows, n] tensor reduced
-// over its last dim on a 64-lane, 512-threads-per-block device: vec = the
-// threads read 4-element vectors (n >= 128), bw threads across a row, bh the
-// block height, split = the row is also divided over the bh wavefronts.
-struct RmsPlan {
-  int vec, bw, bh, split;
-};
-
-inline int last_pow2(int64_t v) {
-  int p = 1;
-  while ((int64_t)p * 2 <= v) p *= 2;
-  return p;
-}
-
-// false when torch would also split rows across blocks (n >= 131072)
-inline bool rms_plan(int64_t rows, int64_t n, RmsPlan& p) {
-  constexpr int kMaxThreads = 512;
-  int64_t dim0 = n;
-  p.vec = dim0 >= 128;
-  if (p.vec) dim0 /= 4;
-  const int d0 = dim0 < kMaxThreads ? last_pow2(dim0) : kMaxThreads;
-  const int d1 = rows < kMaxThreads ? last_pow2(rows) : kMaxThreads;
-  int bw = d0 < kWave ? d0 : kWave;
-  const int bh = d1 < kMaxThreads / bw ? d1 : kMaxThreads / bw;
-  bw = d0 < kMaxThreads / bh ? d0 : kMaxThreads / bh;
-  const int64_t vpt = (n + bw - 1) / bw;
-  p.bw = bw;
-  p.bh = bh;
-  p.split = vpt >= (bh * 16 < 256 ? bh * 16 : 256);
-  return !(p.split && (n + (int64_t)bw * bh - 1) / ((int64_t)bw * bh) >= 256);
-}
 
 // ---- LayerNorm Welford pieces (torch-ROCm's arithmetic) -------------------
 
@@ -283,18 +248,6 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(NormArgs a, int nvec, int
 // Word 3 of a raw buffer resource (the one gemm.hip uses): untyped dword
 // access with range checking against num_records.
 constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ __forceinline__ void unpack4(const u32x2& v, float f[4]) {
-  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
-  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
-}
-
-__device__ __forceinline__ u32x2 pack4(const float f[4]) {
-  u32x2 v;
-  v.x = pack2(f[0], f[1]);
-  v.y = pack2(f[2], f[3]);
-  return v;
-}
 
 // Sixteen lanes per row.  Torch's thread t = 64w + x (wavefront w, lane x)
 // reads the 4-element vectors t, t + 256, ...; here lane l of a row's group

@@ -837,8 +837,15 @@ int launch_direct_r(const RopeArgs& a, hipStream_t st) {
   return launch_status();
 }
 
+// Few positions (decode steps: one position, 40 head rows) take one row per
+// thread: the launch is a latency chain, and R rows per thread put R rows'
+// arithmetic (the norm's reduction and rsqrt) in series on one lane.
+constexpr int64_t kDirectGroupMinThreads = 256 * 256;
+
 template <int MODE, bool NORM>
 int launch_direct(const RopeArgs& a, hipStream_t st) {
+  if (a.B * a.S * (a.Hq + a.Hk) * a.chunks.d <= kDirectGroupMinThreads)
+    return launch_direct_r<MODE, NORM, 1>(a, st);
   switch (group_rows(a.Hq, a.Hk)) {
     case 4: return launch_direct_r<MODE, NORM, 4>(a, st);
     case 2: return launch_direct_r<MODE, NORM, 2>(a, st);

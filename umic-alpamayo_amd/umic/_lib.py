@@ -53,6 +53,9 @@ SIGNATURES: dict[str, list] = {
     "umic_linear_multi_bf16": [_P, _I64, _I64, _I64, _I] + [_P] * 6 + [_I, _P],
     "umic_linear_add_bf16": [_P] * 5 + [_I64] * 7 + [_P],
     "umic_gate_silu_mul_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "umic_rmsnorm_linear_multi_bf16": [_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I]
+                                      + [_P] * 6 + [_P],
+    "umic_add_rmsnorm_gate_silu_mul_bf16": [_P] * 8 + [_I64] * 10 + [_F32, _P],
     "umic_linear_workspace_bytes": [_I64, _I64, _I64],
     "umic_linear_ws_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
     "umic_linear_sk_static_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],

@@ -320,17 +320,66 @@ def _fused_residual_layer_forward(self, hidden_states, position_embeddings=None,
     the transformers decoder layer; extra keyword arguments pass through.
     """
     residual = hidden_states
-    hidden_states = self.input_layernorm(hidden_states)
-    hidden_states, _ = self.self_attn(
-        hidden_states=hidden_states, attention_mask=attention_mask,
-        position_ids=position_ids, past_key_values=past_key_values,
-        use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
+    attn_kwargs = dict(attention_mask=attention_mask, position_ids=position_ids,
+                       past_key_values=past_key_values, use_cache=use_cache,
+                       position_embeddings=position_embeddings, **kwargs)
+    if (getattr(self.self_attn.forward, "__func__", None) is _fused_kv_rope_attention_forward
+            and _foldable_norm(self.input_layernorm, hidden_states)):
+        # decode: the attention folds input_layernorm into its q/k/v GEMV
+        hidden_states, _ = self.self_attn(hidden_states=hidden_states,
+                                          pre_norm=self.input_layernorm, **attn_kwargs)
+    else:
+        hidden_states = self.input_layernorm(hidden_states)
+        hidden_states, _ = self.self_attn(hidden_states=hidden_states, **attn_kwargs)
+    out = _decode_norm_mlp_residual(self.post_attention_layernorm, self.mlp, hidden_states,
+                                    residual)
+    if out is not None:
+        return out
     hidden_states, residual = _add_rmsnorm(self.post_attention_layernorm, hidden_states, residual)
     out = _decode_mlp_residual(self.mlp, hidden_states, residual)
     if out is not None:
         return out
     hidden_states = self.mlp(hidden_states)
     return residual + hidden_states
+
+
+def _foldable_norm(norm: nn.Module, x: torch.Tensor) -> bool:
+    """True if the RMSNorm module `norm` of x can be folded into the decode
+    GEMV that consumes its output: an RMSNorm (class name contains
+    "rmsnorm", 1-D bf16 weight) without hooks, over 1..2 rows whose eager
+    reduction plan the folded norm reproduces, outside autograd."""
+    w = getattr(norm, "weight", None)
+    return ("rmsnorm" in type(norm).__name__.lower() and isinstance(w, torch.Tensor)
+            and not _hooked(norm) and rmsnorm.rmsnorm_eligible(x, w)
+            and rmsnorm.gemv_norm_ok(_rows(x), x.shape[-1]) and not grad_needed(x, w))
+
+
+def _decode_norm_mlp_residual(norm: nn.Module, mlp: nn.Module, x: torch.Tensor,
+                              residual: torch.Tensor):
+    """The decoder layer's tail at decode -- s = residual + x, then
+    s + mlp(norm(s)) -- with the add and norm folded into the P5 GEMV
+    (umic_add_rmsnorm_gate_silu_mul_bf16) and the residual add into the down
+    projection's epilogue: two launches.  None when the MLP is not the fused
+    one or the call is not eligible (the caller then runs the unfolded
+    chain)."""
+    if getattr(mlp.forward, "__func__", None) is not _fused_mlp_forward:
+        return None
+    down = getattr(mlp, "down_proj", None)
+    if _hooked(mlp, down) or not _foldable_norm(norm, x):
+        return None
+    wg, wu = mlp.gate_proj.weight, mlp.up_proj.weight
+    if not (isinstance(down, nn.Linear) and 1 <= _rows(x) <= GEMV_ROWS_DOWN
+            and fused_ffn.p5_eligible(x, wg, wu)
+            and residual.shape == x.shape and residual.dtype == x.dtype
+            and residual.device == x.device
+            and tuple(down.weight.shape) == (x.shape[-1], wg.shape[0])
+            and not grad_needed(x, residual, wg, wu, down.weight, down.bias)):
+        return None
+    h, summed = fused_ffn.add_rmsnorm_gate_silu_mul_hip(x, residual, norm.weight,
+                                                        _norm_eps(norm), wg.t(), wu.t())
+    if not linear.linear_eligible(h, down.weight, down.bias):
+        return summed + down(h)
+    return linear.linear_add_hip(h, down.weight, down.bias, summed)
 
 
 def _decode_mlp_residual(mlp: nn.Module, x: torch.Tensor, residual: torch.Tensor):
@@ -767,14 +816,24 @@ def _attention_interface(module: nn.Module):
     return ALL_ATTENTION_FUNCTIONS.get_interface(impl, eager)
 
 
-def _qkv(attn: nn.Module, x: torch.Tensor) -> list[torch.Tensor]:
-    """The attention's q/k/v projections of x: in the decode regime one GEMV
-    launch for all three (umic_linear_multi_bf16), else each on its own."""
+def _qkv(attn: nn.Module, x: torch.Tensor, pre_norm: nn.Module | None = None) -> list[torch.Tensor]:
+    """The attention's q/k/v projections of pre_norm(x) (of x when pre_norm is
+    None): in the decode regime one GEMV launch for all three
+    (umic_linear_multi_bf16), with the norm folded in when it can be
+    (umic_rmsnorm_linear_multi_bf16); else the norm, then each projection on
+    its own."""
     mods = (attn.q_proj, attn.k_proj, attn.v_proj)
-    if (1 <= _rows(x) <= GEMV_MAX_ROWS and all(isinstance(m, nn.Linear) for m in mods)
+    gemv = (1 <= _rows(x) <= GEMV_MAX_ROWS and all(isinstance(m, nn.Linear) for m in mods)
             and not _hooked(*mods)
             and all(linear.linear_eligible(x, m.weight, m.bias) for m in mods)
-            and not grad_needed(x, *(m.weight for m in mods), *(m.bias for m in mods))):
+            and not grad_needed(x, *(m.weight for m in mods), *(m.bias for m in mods)))
+    if pre_norm is not None:
+        if gemv and _foldable_norm(pre_norm, x):
+            return linear.rmsnorm_linear_multi_hip(x, pre_norm.weight, _norm_eps(pre_norm),
+                                                   [m.weight for m in mods],
+                                                   [m.bias for m in mods])
+        x = pre_norm(x)
+    if gemv:
         return linear.linear_multi_hip(x, [m.weight for m in mods], [m.bias for m in mods])
     return [_linear(m, x) for m in mods]
 
@@ -794,7 +853,8 @@ def _head_norms(module: nn.Module, q: torch.Tensor):
 
 
 def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
-                                     attention_mask=None, past_key_values=None, **kwargs):
+                                     attention_mask=None, past_key_values=None, pre_norm=None,
+                                     **kwargs):
     """Text attention whose q/k norms, RoPE and KV-cache append are one launch.
 
     The projections, attention and output projection are the module's own
@@ -808,6 +868,10 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
       (``umic_qk_rmsnorm_rope_bf16``), then the cache's own ``update``;
     * otherwise the module's norms, ``apply_rotary_pos_emb`` and ``update``.
 
+    pre_norm: the decoder layer's input norm, applied to hidden_states first
+    (folded into the q/k/v GEMV at decode); the fused decoder-layer forward
+    passes it.
+
     Training, or autograd through any weight or the input, runs the class
     forward.
     """
@@ -816,6 +880,8 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
     if self.training or grad_needed(hidden_states, self.q_proj.weight, self.k_proj.weight,
                                     self.v_proj.weight, getattr(self.q_norm, "weight", None),
                                     getattr(self.k_norm, "weight", None)):
+        if pre_norm is not None:
+            hidden_states = pre_norm(hidden_states)
         return type(self).forward(self, hidden_states, position_embeddings, attention_mask,
                                   past_key_values=past_key_values, **kwargs)
     layer = None
@@ -826,7 +892,7 @@ def _fused_kv_rope_attention_forward(self, hidden_states, position_embeddings,
             layer = None
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    q_raw, k_raw, v = (t.view(hidden_shape) for t in _qkv(self, hidden_states))
+    q_raw, k_raw, v = (t.view(hidden_shape) for t in _qkv(self, hidden_states, pre_norm))
     v = v.transpose(1, 2)
     cos, sin = position_embeddings
     q, k = q_raw.transpose(1, 2), k_raw.transpose(1, 2)

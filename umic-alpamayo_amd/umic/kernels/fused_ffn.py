@@ -71,6 +71,41 @@ def gate_silu_mul_hip(x: torch.Tensor, w_gate: torch.Tensor,
     return out.reshape(*shape[:-1], N)
 
 
+def add_rmsnorm_gate_silu_mul_hip(x: torch.Tensor, residual: torch.Tensor,
+                                  norm_weight: torch.Tensor, eps: float, w_gate: torch.Tensor,
+                                  w_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(gate_silu_mul(rmsnorm(bf16(x + residual))), bf16(x + residual)) in one
+    launch (umic_add_rmsnorm_gate_silu_mul_bf16): the decode step's
+    post-attention residual add and RMSNorm folded into the P5 GEMV,
+    bit-identical to ``rmsnorm.add_rmsnorm_hip`` then ``gate_silu_mul_hip``.
+    x and residual have 1..GEMV_NORM_MAX_ROWS rows that
+    ``rmsnorm.gemv_norm_ok`` accepts; w_gate / w_up are [K, N] as for
+    ``gate_silu_mul_hip``."""
+    from umic.kernels import rmsnorm
+
+    require_device(x, residual, norm_weight, w_gate, w_up)
+    wg, wu = _as_nk(w_gate), _as_nk(w_up)
+    if not p5_eligible(x, wg, wu):
+        raise ValueError(f"add_rmsnorm_gate_silu_mul_hip: unsupported shape x{tuple(x.shape)} "
+                         f"w{tuple(w_gate.shape)}")
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError(f"residual shape {tuple(residual.shape)} != x shape {tuple(x.shape)}")
+    x2d, r2d = _gemm_ready(rows2d(x)), rows2d(residual).contiguous()
+    M, K = x2d.shape
+    if not rmsnorm.gemv_norm_ok(M, K) or tuple(norm_weight.shape) != (K,):
+        raise ValueError(f"add_rmsnorm_gate_silu_mul_hip: {M} x {K} rows are not a foldable norm")
+    N = wg.shape[0]
+    nw = norm_weight.contiguous()
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    summed = torch.empty((M, K), dtype=x.dtype, device=x.device)
+    with _lib.device_of(x):
+        _lib.call("umic_add_rmsnorm_gate_silu_mul_bf16", x2d.data_ptr(), r2d.data_ptr(),
+                  nw.data_ptr(), None, summed.data_ptr(), wg.data_ptr(), wu.data_ptr(),
+                  out.data_ptr(), M, N, K, ld(x2d), ld(r2d), K, K, ld(wg), ld(wu), N,
+                  float(eps), _lib.stream_of(x))
+    return out.reshape(*x.shape[:-1], N), summed.reshape(x.shape)
+
+
 def gate_silu_mul(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     """Best available implementation for the P5 motif (reference
     src/umic/kernels/fused_ffn.py:121-126): the HIP kernel for GPU tensors

@@ -116,6 +116,43 @@ def linear_multi_hip(x: torch.Tensor, weights, biases=None) -> list[torch.Tensor
     return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
 
 
+def rmsnorm_linear_multi_hip(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weights,
+                             biases=None) -> list[torch.Tensor]:
+    """[rmsnorm(x) @ w.T + b for each (w, b)] in one launch
+    (umic_rmsnorm_linear_multi_bf16): the decode step's input RMSNorm folded
+    into the q/k/v GEMV, bit-identical to ``rmsnorm_hip`` then
+    ``linear_multi_hip``.  x has 1..GEMV_NORM_MAX_ROWS rows whose norm plan
+    ``rmsnorm.gemv_norm_ok`` accepts."""
+    from umic.kernels import rmsnorm
+
+    biases = list(biases) if biases is not None else [None] * len(weights)
+    require_device(x, norm_weight, *weights, *[b for b in biases if b is not None])
+    if not 1 <= len(weights) <= 3 or len(biases) != len(weights):
+        raise ValueError("rmsnorm_linear_multi_hip: one to three linears")
+    x2d = _gemm_ready(rows2d(x))
+    M, K = x2d.shape
+    if not rmsnorm.gemv_norm_ok(M, K) or tuple(norm_weight.shape) != (K,):
+        raise ValueError(f"rmsnorm_linear_multi_hip: {M} x {K} rows are not a foldable norm")
+    for w, b in zip(weights, biases):
+        if not linear_eligible(x, w, b):
+            raise ValueError(f"rmsnorm_linear_multi_hip: unsupported shape x{tuple(x.shape)} "
+                             f"w{tuple(w.shape)}")
+    nw = norm_weight.contiguous()
+    ws = [_gemm_ready(w) for w in weights]
+    bs = [None if b is None else b.contiguous() for b in biases]
+    outs = [torch.empty((M, w.shape[0]), dtype=x.dtype, device=x.device) for w in ws]
+    n = len(ws)
+    P, I64 = ctypes.c_void_p * n, ctypes.c_int64 * n
+    with _lib.device_of(x):
+        _lib.call("umic_rmsnorm_linear_multi_bf16", x2d.data_ptr(), nw.data_ptr(), None, M, K,
+                  ld(x2d), K, float(eps), n,
+                  P(*[w.data_ptr() for w in ws]), P(*[_lib.ptr(b) for b in bs]),
+                  P(*[o.data_ptr() for o in outs]), I64(*[w.shape[0] for w in ws]),
+                  I64(*[ld(w) for w in ws]), I64(*[w.shape[0] for w in ws]),
+                  _lib.stream_of(x))
+    return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
+
+
 def linear_add_hip(x: torch.Tensor, weight: torch.Tensor, bias, residual: torch.Tensor):
     """residual + (x @ weight.T + bias), rounded as the eager chain rounds
     (the linear's bf16 output, then the bf16 sum), in one decode-GEMV launch

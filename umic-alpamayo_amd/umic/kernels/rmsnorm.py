@@ -62,6 +62,54 @@ def add_rmsnorm_hip(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tenso
     return normed.reshape(shape), summed.reshape(shape)
 
 
+def _last_pow2(v: int) -> int:
+    p = 1
+    while p * 2 <= v:
+        p *= 2
+    return p
+
+
+# Rows and LDS limit of the decode launches that fold the norm into a GEMV
+# (umic_rmsnorm_linear_multi_bf16, umic_add_rmsnorm_gate_silu_mul_bf16).
+GEMV_NORM_MAX_ROWS = 2
+GEMV_NORM_MAX_LDS = 64 << 10
+
+
+def wide_plan(rows: int, n: int) -> tuple[int, int] | None:
+    """(bw, k4) of torch's RMSNorm reduction plan (Reduce.cuh's
+    setReduceConfig for a contiguous fp32 [rows, n] reduced over n, as the
+    library's ``rms_plan`` restates it) when the library runs it as its wide
+    single-block kernel -- 4-vectors, no row split, bw >= 128 reducing
+    threads with k4 <= 8 vectors each -- else None.  The GEMV-folded norms
+    reproduce exactly this plan."""
+    if rows < 1 or n < 128 or n % 4:
+        return None
+    dim0 = n // 4
+    d0 = _last_pow2(dim0) if dim0 < 512 else 512
+    d1 = _last_pow2(rows) if rows < 512 else 512
+    bw = d0 if d0 < 64 else 64
+    bh = d1 if d1 < 512 // bw else 512 // bw
+    bw = d0 if d0 < 512 // bh else 512 // bh
+    vpt = -(-n // bw)
+    if vpt >= min(bh * 16, 256) or bw < 128:
+        return None
+    k4 = -(-(n // 4) // bw)
+    return (bw, k4) if k4 <= 8 else None
+
+
+# 4-vectors per thread and row the folded norm holds in registers (its 256
+# threads play bw reducing threads with k4 vectors each).
+GEMV_NORM_MAX_PV = 4
+
+
+def gemv_norm_ok(rows: int, n: int) -> bool:
+    """True if a decode GEMV over rows x n can fold the RMSNorm of its input."""
+    if not (1 <= rows <= GEMV_NORM_MAX_ROWS and n % 8 == 0 and rows * n * 2 <= GEMV_NORM_MAX_LDS):
+        return False
+    plan = wide_plan(rows, n)
+    return plan is not None and (2 if plan[0] > 256 else 1) * plan[1] <= GEMV_NORM_MAX_PV
+
+
 # Names of the reference's wrappers (src/umic/kernels/rmsnorm.py:53, :103),
 # kept so code written against that API runs unchanged on this runtime.
 rmsnorm_triton = rmsnorm_hip
