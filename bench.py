@@ -36,9 +36,10 @@ count (copy_us, of_copy = copy time / kernel time), and copy_ceiling_gbps /
 of_copy give the same for the six together;
 mlp_prefill_ms = gate_silu_mul + down_proj; roofline = the dominant kernel
 (by time) of the step, its traffic (HBM bytes per launch) measured at the
-end of the run, after every timed step, by two rocprofv3 --pmc child runs of --pmc-probe (FETCH_SIZE,
+end of the run, after every timed step, by rocprofv3 --pmc child runs of --pmc-probe (FETCH_SIZE,
 WRITE_SIZE, scaled by a device copy of known size; the committed PMC summary
-when the profiler is absent or --no-traffic is given); cpu_baseline = the reference's own CPU path (HF's
+when the profiler is absent or --no-traffic is given), and its clock_ghz from
+a GRBM_GUI_ACTIVE pass of the same probe; cpu_baseline = the reference's own CPU path (HF's
 eager Qwen3-VL modules, RoPE functions and the eager P5 chain in torch, bf16,
 on the host cores) over all five BASELINE configs at full size, value in GB/s
 over the norm/RoPE ops as for the GPU; cpu_oracle = the scalar C oracle (one
@@ -461,12 +462,15 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"  # the HIP runtime's device copy (the pr
 def measure_traffic(name: str):
     """HBM bytes per launch of bench entry `name`, measured in this run.
 
-    Two child runs of ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) over
+    Child runs of ``rocprofv3 --pmc FETCH_SIZE`` (then ``WRITE_SIZE``) over
     this script's ``--pmc-probe`` mode, restricted to the calibration copy and
     that kernel (one launch each, after a 1 GiB fill that evicts the Infinity
     Cache).  Each counter is scaled by what it reads for the copy, which moves
-    exactly COPY_BYTES each way.  Returns (bytes, scales, None) or
-    (None, None, reason) when the profiler is absent or a pass fails.
+    exactly COPY_BYTES each way.  A third pass reads GRBM_GUI_ACTIVE, the GPU
+    clock cycles the launch kept the graphics engine busy (summed over the
+    XCDs), from which the caller derives the clock the kernel ran at.
+    Returns (bytes, counters, None) or (None, None, reason) when the profiler
+    is absent or a pass fails.
     """
     import csv
     import glob
@@ -481,7 +485,7 @@ def measure_traffic(name: str):
     env = dict(os.environ, TMPDIR="/tmp")
     vals = {}
     with tempfile.TemporaryDirectory(prefix="umic_pmc_", dir="/tmp") as tmp:
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        for counter in ("FETCH_SIZE", "WRITE_SIZE", "GRBM_GUI_ACTIVE"):
             out = os.path.join(tmp, counter)
             # a pass takes a few seconds; the kill bound keeps a stuck profiler
             # from holding the run
@@ -498,7 +502,9 @@ def measure_traffic(name: str):
                 vals[counter] = pmc_copy_and_kernel(csv.DictReader(f), frag)
             if vals[counter] is None:
                 return None, None, f"{counter} pass: calibration copy or kernel not found"
-    return (*calibrated_traffic(vals["FETCH_SIZE"], vals["WRITE_SIZE"]), None)
+    nbytes, info = calibrated_traffic(vals["FETCH_SIZE"], vals["WRITE_SIZE"])
+    info["grbm_gui_active"] = vals["GRBM_GUI_ACTIVE"][1]
+    return nbytes, info, None
 
 
 def pmc_copy_and_kernel(rows, frag: str):
@@ -956,7 +962,7 @@ def main() -> int:
                          "(after the calibration copy)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="take roofline.traffic from the committed PMC summary instead of "
-                         "measuring it (two rocprofv3 --pmc child runs); use when this run "
+                         "measuring it (three rocprofv3 --pmc child runs); use when this run "
                          "is itself under rocprofv3")
     ap.add_argument("--copy-ceiling", action="store_true",
                     help="time plain device copies of the norm/RoPE byte counts")
@@ -1082,6 +1088,15 @@ def main() -> int:
                                   f"{dom_name}; counters scaled by a {COPY_BYTES >> 20} MiB "
                                   "device copy")
         roof["traffic_counters"] = scales
+        # the clock: GUI-active cycles per XCD (32 CUs each) over the
+        # kernel's timed duration
+        import torch
+
+        xcds = max(1, torch.cuda.get_device_properties(0).multi_processor_count // 32)
+        roof["clock_ghz"] = round(scales["grbm_gui_active"] / xcds / (dom["us"] * 1e3), 3)
+        roof["clock_source"] = (f"GRBM_GUI_ACTIVE {scales['grbm_gui_active']:.0f} over {xcds} "
+                                f"XCDs / {dom['us']} us (rocprofv3 --pmc GRBM_GUI_ACTIVE pass "
+                                "of the same probe)")
     else:
         roof["traffic"] = load_traffic(dom_name)
         roof["traffic_source"] = (f"committed profiles/traffic_{dom_name}.json (not measured "
