@@ -195,3 +195,40 @@ def test_decoder_layer_decode_folds_both_norms(monkeypatch):
     finally:
         integrate.unfuse_rope()
         integrate.unfuse_mlps(layer)
+
+
+def test_folded_decode_step_in_a_captured_graph():
+    """The folded decode step of a config-5 layer (no cache) captured in one
+    HIP graph: four replays, with eager work and synchronisations between
+    them, equal the eager fused step bit for bit."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    layer, rot = qwen3_decoder_layer(DEV)
+    torch.manual_seed(13)
+    x = torch.randn(1, 1, 4096).to(torch.bfloat16).to(DEV)
+    cs = rot(x, torch.tensor([[5]], device=DEV))
+    try:
+        with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION,
+                                           SDPBackend.EFFICIENT_ATTENTION]):
+            assert integrate.fuse_mlps(layer) == 1 and integrate.fuse_linears(layer) == 2
+            assert integrate.fuse_rmsnorms(layer) == 4 and integrate.fuse_add_rmsnorm(layer) == 1
+            assert integrate.fuse_text_rope() and integrate.fuse_kv_rope(layer) == 1
+            ref = layer(x, position_embeddings=cs)
+            torch.cuda.synchronize()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                layer(x, position_embeddings=cs)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = layer(x, position_embeddings=cs)
+            for i in range(4):
+                print(f"folded decode graph replay {i}", flush=True)
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, ref), i
+                _ = (x.float() * 2).sum().item()  # eager work between replays
+    finally:
+        integrate.unfuse_rope()
+        integrate.unfuse_mlps(layer)
