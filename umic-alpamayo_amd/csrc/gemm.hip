@@ -45,7 +45,9 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <map>
 #include <mutex>
+#include <utility>
 
 namespace umic {
 namespace {
@@ -1569,13 +1571,26 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_norm_kernel(GemvJob job)
   }
 }
 
-// Workgroups of a persistent launch that fit on the device at once.
-template <typename Kern>
-int64_t resident_grid(Kern kern, size_t lds) {
+// Workgroups of a persistent launch that fit on the device at once.  The
+// occupancy query is cached per (kernel, LDS size): a decode loop asks the
+// same few every step.
+int64_t resident_grid(void (*kern)(GemvJob), size_t lds) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, size_t>, int> cache;
+  const auto key = std::make_pair(reinterpret_cast<const void*>(kern), lds);
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kGemvWaves * 64, lds) !=
-          hipSuccess || per_cu < 1)
-    per_cu = 1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) per_cu = it->second;
+  }
+  if (per_cu == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kGemvWaves * 64, lds) !=
+            hipSuccess || per_cu < 1)
+      per_cu = 1;
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = per_cu;
+  }
   return (int64_t)device_cus() * per_cu;
 }
 
