@@ -46,7 +46,10 @@ over the norm/RoPE ops as for the GPU; cpu_oracle = the scalar C oracle (one
 core) on a bounded quarter-row sample of the norm/RoPE workload.
 layer = BASELINE config 5, one Qwen3-VL decoder layer eager vs fused at
 prefill M=3100 and decode M=1 (plus the fused decode step replayed from a
-HIP graph); vit_encoder = BASELINE config 4 in context, the Qwen3-VL vision
+HIP graph); decode_gemv = that decode step's four GEMV launches on weights
+rotated past every cache (as in a many-layer decode), each beside a plain
+streaming read of the same weight bytes (umic_stream_read; of_read = read
+time / GEMV time); vit_encoder = BASELINE config 4 in context, the Qwen3-VL vision
 encoder (4 blocks, 16384 tokens, hidden 1280) eager vs with the vision
 fusions injected; --no-layer skips both.  kv_cache = text RoPE fused with the
 in-place KV-cache append against RoPE + two slice copies, at prefill and at a
@@ -629,6 +632,104 @@ def same_bytes_copy(moved: int, steps: int) -> float:
     return e0.elapsed_time(e1) / steps * 1e3
 
 
+def _ring_len(nbytes: int) -> int:
+    """Copies of an nbytes operand set so that a set returns only after
+    >= 640 MB of other reads: the 256 MB Infinity Cache serves none of it."""
+    return max(2, min(24, int(-(-640e6 // nbytes))))
+
+
+def _graph_us(fn, n: int, reps: int) -> float:
+    """Microseconds per launch of fn(i), i cycling over n ring slots, from a
+    HIP graph of `reps` such launches (as a decode step replays them: the
+    host's per-call cost, which exceeds these kernels' run time, stays out),
+    replayed three times between two events."""
+    import torch
+
+    for i in range(n):
+        fn(i)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(reps):
+            fn(i % n)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / (3 * reps) * 1e3
+    del graph
+    return us
+
+
+def stream_read_us(nbytes: int, reps: int) -> float:
+    """Microseconds of one plain streaming read of nbytes (umic_stream_read),
+    graph-replayed over a ring of buffers that no cache holds: the practical
+    ceiling of a kernel that reads those bytes once."""
+    import torch
+
+    from umic import _lib
+
+    nbytes = nbytes // 16 * 16
+    n = _ring_len(nbytes)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255)
+            for _ in range(n)]
+    fold = torch.empty(_lib.UMIC_STREAM_READ_GRID, dtype=torch.int32, device="cuda")
+    return _graph_us(lambda i: _lib.call("umic_stream_read", bufs[i].data_ptr(), nbytes,
+                                         fold.data_ptr(), _lib.stream_of(fold)), n, reps)
+
+
+def decode_gemv_step(reps: int = 60) -> dict:
+    """The BASELINE config-5 decode step's four weight streams (one row, the
+    library's GEMV launches exactly as the fused layer issues them) on
+    weights rotated so that no cache holds them -- as in a decode over a
+    many-layer model -- each beside umic_stream_read over the same weight
+    bytes: of_read = read time / GEMV time (1.0 = as fast as reading the
+    weights once)."""
+    import torch
+
+    from umic.kernels import fused_ffn, linear
+
+    H, KV, FF, eps = 4096, 1024, 12288, 1e-6
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    x, r = _bf(1, H, gen=gen), _bf(1, H, gen=gen)
+    nw = _bf(H, scale=0.1, shift=1.0, gen=gen)
+    h = _bf(1, FF, gen=gen)
+
+    def site(shapes, launch):
+        nbytes = sum(2 * a * b for a, b in shapes)
+        n = _ring_len(nbytes)
+        ws = [[_bf(a, b, scale=0.02, gen=gen) for a, b in shapes] for _ in range(n)]
+        us = _graph_us(lambda i: launch(ws[i]), n, reps)
+        del ws
+        torch.cuda.empty_cache()
+        read = stream_read_us(nbytes, reps)
+        torch.cuda.empty_cache()
+        return {"us": round(us, 2), "read_us": round(read, 2), "of_read": round(read / us, 3),
+                "weight_mb": round(nbytes / 1e6, 1), "gbps": round(nbytes / us / 1e3, 1)}
+
+    res = {
+        "qkv_norm": site([(H, H), (KV, H), (KV, H)],
+                         lambda w: linear.rmsnorm_linear_multi_hip(x, nw, eps, w)),
+        "o_proj": site([(H, H)], lambda w: linear.linear_hip(x, w[0])),
+        "add_norm_gate_silu_mul": site(
+            [(FF, H), (FF, H)],
+            lambda w: fused_ffn.add_rmsnorm_gate_silu_mul_hip(x, r, nw, eps, w[0].t(), w[1].t())),
+        "down_proj_add": site([(H, FF)], lambda w: linear.linear_add_hip(h, w[0], None, x)),
+    }
+    sites = list(res.values())
+    res["sum_us"] = round(sum(v["us"] for v in sites), 2)
+    res["read_sum_us"] = round(sum(v["read_us"] for v in sites), 2)
+    return res
+
+
 def _config5_layer():
     """BASELINE config 5 text decoder layer in bf16 on the GPU with random
     N(0, 0.02) weights (norms 1 + N(0, 0.1)), its rotary embedding and the
@@ -970,6 +1071,9 @@ def main() -> int:
                     help="time the ViT projection sites, this library against hipBLASLt")
     ap.add_argument("--decode-layer", action="store_true",
                     help="run ten fused config-5 decode steps (for a kernel trace) and exit")
+    ap.add_argument("--decode-gemv", action="store_true",
+                    help="time the config-5 decode GEMVs on cold weights against plain reads "
+                         "of the same bytes, print them and exit")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the decoder-layer (config 5) and vision-encoder (config 4) "
                          "timings")
@@ -995,6 +1099,15 @@ def main() -> int:
         return vit_sites()
     if args.decode_layer:
         return decode_layer()
+    if args.decode_gemv:
+        import torch
+
+        from umic import _lib
+
+        _lib.load()
+        torch.cuda.set_device(0)
+        print(json.dumps({"decode_gemv": decode_gemv_step()}), flush=True)
+        return 0
 
     import torch
 
@@ -1075,6 +1188,7 @@ def main() -> int:
     # this process's later kernels ran slower (the fused ViT encoder 25 against
     # 10 ms), so the PMC passes come last
     layer = None if args.no_layer else layer_step()
+    decode = None if args.no_layer else decode_gemv_step()
     vit = None if args.no_layer else vit_step()
     kv = None if args.no_kv_cache else kv_cache_step()
     cpu_base = None if args.no_cpu_baseline else cpu_reference(args.cpu_budget_s)
@@ -1134,6 +1248,7 @@ def main() -> int:
         "kernels": kern,
         "roofline": roof,
         "layer": layer,
+        "decode_gemv": decode,
         "vit_encoder": vit,
         "kv_cache": kv,
         "cpu_baseline": cpu_base,

@@ -390,6 +390,19 @@ int umic_add_rmsnorm_gate_silu_mul_bf16(const void* x, const void* r, const void
                                         int64_t lds, int64_t ldwg, int64_t ldwu, int64_t ldo,
                                         float eps, void* stream);
 
+/*
+ * Measurement helper: reads `bytes` bytes at p once (16-byte non-temporal
+ * loads; p 16-byte aligned, bytes a multiple of 16, else
+ * UMIC_ERR_UNSUPPORTED) and writes one xor-fold word per workgroup to
+ * fold[0 .. UMIC_STREAM_READ_GRID) (4-byte aligned).  Its time is the
+ * practical ceiling of a kernel that streams the same bytes from HBM, the
+ * yardstick bench.py holds the decode GEMVs (one pass over their weights)
+ * against.  No counterpart in the reference; nothing on the fused path
+ * calls it.
+ */
+#define UMIC_STREAM_READ_GRID 2048
+int umic_stream_read(const void* p, int64_t bytes, void* fold, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

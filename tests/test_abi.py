@@ -39,7 +39,7 @@ def test_header_declares_expected_entry_points():
               "umic_linear_multi_bf16", "umic_linear_add_bf16",
               "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
               "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_linear_sk_static_bf16",
-              "umic_version", "umic_error_string"):
+              "umic_stream_read", "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -108,6 +108,13 @@ def test_argument_rejection_before_launch(lib):
     assert sk(fake, fake, None, fake, 300, 4096, 12288, 12288, 12288, 4096, 3, None) == E_ARG
     assert sk(fake, fake, None, fake, 300, 4092, 12288, 12288, 12288, 4092, 0, None) == E_UNS
     assert sk(fake, fake, fake + 2, fake, 300, 4096, 12288, 12288, 12288, 4096, 0, None) == E_UNS
+    # the read-ceiling helper: negative / misaligned sizes and pointers
+    rd = lib.umic_stream_read
+    assert rd(fake, -16, fake, None) == E_ARG
+    assert rd(None, 0, None, None) == 0
+    assert rd(None, 4096, fake, None) == E_ARG
+    assert rd(fake, 4100, fake, None) == E_UNS
+    assert rd(fake + 8, 4096, fake, None) == E_UNS
     assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
                                        None) == E_ARG
     # stream-K linear: same validation; a negative workspace size is rejected

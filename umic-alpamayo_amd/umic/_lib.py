@@ -31,6 +31,7 @@ UMIC_ROPE_VISION = 1
 UMIC_ACT_NONE = 0
 UMIC_ACT_GELU = 1
 UMIC_ACT_GELU_TANH = 2
+UMIC_STREAM_READ_GRID = 2048  # fold words umic_stream_read writes
 
 _P, _I64, _F32, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
 
@@ -59,6 +60,7 @@ SIGNATURES: dict[str, list] = {
     "umic_linear_workspace_bytes": [_I64, _I64, _I64],
     "umic_linear_ws_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
     "umic_linear_sk_static_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    "umic_stream_read": [_P, _I64, _P, _P],
     "umic_version": [],
     "umic_error_string": [_I],
 }
