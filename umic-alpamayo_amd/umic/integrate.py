@@ -90,15 +90,19 @@ GEMV_ROWS_DOWN = 2    # the MLP's down projection (and its residual epilogue)
 #     3000: 1.17, 3100: 0.88, 3300: 0.98, 3500: 1.03, 3800: 1.03, 4096: 1.07
 #   plain q/o_proj linear (K = N = 4096):
 #     M = 64: 5.1, 256: 4.1, 1024: 2.05, 2048: 1.37, 2900: 1.06, 3000: 1.07,
-#     3100: 1.00, 3300: 1.04, 3500: 1.05, 3800: 0.98, 4096: 1.10, 8192: 1.10
+#     3100: 1.00, 3300: 1.04, 3500: 1.05, 3800: 0.98, 4096: 1.10, 8192: 1.10;
+#     finer, two passes on one box: 3073: 1.01 / 0.97, 3100: 1.02 / 0.99,
+#     3136: 1.00 / 1.00, 3200: 1.01 / 1.01, 3264: 1.03 / 1.08, 3328: 1.07 /
+#     1.13, 3700: 1.01 / 1.03, 3800: 1.07 / 1.06, 3840: 1.11 / 1.08, 3900:
+#     1.04 / 0.97
 # The 256 x 256 tiles leave most CUs idle below a few thousand rows, where
 # hipBLASLt picks smaller tiles; from there both run at the chip's power
 # cap and the vendor's kernel choice decides.  So each site takes its tiled
 # kernel only where it stops losing (the reference's own rule: fuse a site
 # only where measured faster, integrate.py:80-91): P5 from 256 rows, fc1 +
 # GELU from 2048, down_proj in the 13-tile-row band 3072..3328 (where
-# hipBLASLt's pick is slow); the plain q/o linear never (None): a tie at
-# 3100 rows and one 2% win at 3800 among 4-10% losses.
+# hipBLASLt's pick is slow); the plain q/o linear never (None): a tie within
+# +-3% from 3073 to 3200 rows and no row count where it wins on both passes.
 TILED_MIN_ROWS_MLP = 256
 TILED_MIN_ROWS_GELU_MLP = 2048
 TILED_MIN_ROWS_DOWN = 3072
