@@ -277,10 +277,10 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
  * numerics, shape rules and results as umic_linear_ws_bf16 with a large
  * enough workspace; shapes the data-parallel kernel or the GEMV serve run
  * those, as there.  A shape whose stream-K workspace
- * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 85 output tiles
- * of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  At N = 4096,
- * K = 12288 (the MLP down projection) that admits M <= 1280; M from 1281
- * to 2816 (stream-K, over 64 MiB) needs umic_linear_ws_bf16, and the
+ * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 127 output
+ * tiles of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  At
+ * N = 4096, K = 12288 (the MLP down projection) that admits M <= 1792; M
+ * from 1793 to 2816 (stream-K, over 64 MiB) needs umic_linear_ws_bf16, and the
  * BASELINE prefill (M = 3100, 208 tiles) runs the data-parallel kernel
  * here too.  The device's first call clears the scratch's
  * counter region with a kernel (no memset); every launch leaves it cleared.

@@ -2,9 +2,10 @@
 static scratch (no workspace argument, no allocation).
 
 Through the C ABI, against umic_linear_ws_bf16 on a caller workspace (the
-same kernel, so bit for bit): two stream-K calls in a row on one stream,
-the second smaller and with a bias and the GELU epilogue, so it runs on
-the scratch the first left behind; a few-row (GEMV) and a data-parallel
+same kernel, so bit for bit): stream-K calls in a row on one stream, each
+smaller than the one before (the first, 96 tiles, near the scratch's
+limit; the last with a bias and the GELU epilogue), so each runs on the
+scratch the previous left behind; a few-row (GEMV) and a data-parallel
 shape, which need no scratch and pass through to umic_linear_bf16; and a
 shape whose workspace exceeds the 64 MiB scratch, rejected before any
 launch.
@@ -53,7 +54,8 @@ def _with_workspace(x, w, b, act):
 
 
 def test_static_scratch_matches_the_workspace_entry_point():
-    calls = [((300, 4096, 12288), 1, False, _lib.UMIC_ACT_NONE),
+    calls = [((1536, 4096, 12288), 1, False, _lib.UMIC_ACT_NONE),
+             ((300, 4096, 12288), 6, False, _lib.UMIC_ACT_NONE),
              ((32, 2048, 12288), 2, True, _lib.UMIC_ACT_GELU)]
     for (M, N, K), seed, bias, act in calls:
         need = _lib.lib().umic_linear_workspace_bytes(M, N, K)
@@ -87,7 +89,7 @@ def test_shapes_without_scratch_pass_through(M, N, K):
 
 
 def test_shape_beyond_the_scratch_is_rejected():
-    M, N, K = 1536, 4096, 12288  # 96 output tiles, 75 MB of partials
+    M, N, K = 2048, 4096, 12288  # 128 output tiles: 64 MiB of partials plus the counters
     assert _lib.lib().umic_linear_workspace_bytes(M, N, K) > SCRATCH_BYTES
     x, w, _ = _operands(M, N, K, 4)
     out = torch.zeros(M, N, dtype=torch.bfloat16, device=DEV)

@@ -852,22 +852,27 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm_w4_kernel(GemmArgs g) {
 // order) evenly between them, stream-K style.  A tile whose K range one
 // workgroup covers is stored directly.  A split tile's segments (the main
 // one, then its tail pieces in K order) are reduced by whichever workgroup
-// arrives last: the others store their fp32 partial in the tile's segment
-// slot and count themselves "written"; the last waits for that count --
-// every workgroup it waits for has already arrived, so it is running and
-// finishes its store without waiting on anything -- then sums the segments
-// in segment order (deterministic whatever the arrival order), applies the
-// epilogue and resets the tile's two counters, so the workspace is
-// all-zero counters again after every launch.
+// arrives last: the others store their fp32 partial in the tile's slot for
+// their arrival order (the first arriver slot 0, the second slot 1; the last
+// stores none, so a tile of kSkMaxSeg segments needs kSkSlots slots), tag
+// the slot with their segment index and count themselves "written"; the
+// last waits for that count -- every workgroup it waits for has already
+// arrived, so it is running and finishes its store without waiting on
+// anything -- then, through the tags, sums the segments in segment order
+// (deterministic whatever the arrival order), applies the epilogue and
+// resets the tile's two counters, so the workspace is all-zero counters
+// again after every launch.
 struct SkArgs {
   int* counters;   // [2 * T]: arrived, written (zero between launches)
   int* status;     // sticky status word (0: every wait completed)
-  f32x4_t* slots;  // [T][kSkMaxSeg][kSlotVec]: segment partials
+  int* tags;       // [T][kSkSlots]: the segment whose partial a slot holds
+  f32x4_t* slots;  // [T][kSkSlots][kSlotVec]: partials, by arrival order
   int T, KT, ks;   // tiles, K steps per tile, main steps per tile
   int G;           // workgroups (T main + G - T tail)
 };
 constexpr int kSlotVec = kBM * kBW / 4;  // f32x4 per partial tile (256 KB)
 constexpr int kSkMaxSeg = 3;             // segments per tile (checked on the host)
+constexpr int kSkSlots = kSkMaxSeg - 1;  // stored partials per tile
 // Workspace layout: the tile counters in a region of fixed size, then the
 // partial slots.  One workspace serves calls of any shape in turn, so no
 // call's slots may overlap another call's counters: with the counter region
@@ -875,10 +880,13 @@ constexpr int kSkMaxSeg = 3;             // segments per tile (checked on the ho
 // where a later call with more tiles kept (and trusted) zero counters.
 // The region also holds one sticky status word after the counters, at byte
 // kSkStatusOffset: a last arriver whose wait gives up (below) stores 1 + its
-// tile index there; nothing else writes it and no launch clears it.
+// tile index there; nothing else writes it and no launch clears it.  The
+// slot tags follow it; a tag is written before its slot is counted and read
+// only after, so tags need no clearing.
 constexpr int kSkMaxTiles = 1024;        // stream-K needs fewer tiles than CUs
 constexpr int64_t kSkStatusOffset = 2 * kSkMaxTiles * (int64_t)sizeof(int);
-constexpr int64_t kSkCounterBytes = kSkStatusOffset + 256;
+constexpr int64_t kSkTagOffset = kSkStatusOffset + 256;
+constexpr int64_t kSkCounterBytes = kSkTagOffset + kSkSlots * kSkMaxTiles * (int64_t)sizeof(int);
 static_assert(kSkStatusOffset == UMIC_SK_STATUS_OFFSET, "status word offset of the C ABI");
 static_assert(kSkCounterBytes % 256 == 0, "partial slots stay 256-byte aligned");
 
@@ -1001,11 +1009,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
     // dword each, lane-contiguous), so publishing one needs no L2
     // write-back and reading one no L2 invalidate (either would stall every
     // CU of the XCD): a partial is visible device-wide once its stores have
-    // completed.  Layout: [segment][block a*4+b][element e][thread].
+    // completed.  Layout: [slot][block a*4+b][element e][thread].
     if (order < nseg - 1) {
-      // Not last: publish this segment's partial, then count it.
-      f32x4_t* const dst = reinterpret_cast<f32x4_t*>(s.slots + (int64_t)t * kSkMaxSeg * kSlotVec +
-                                                      (int64_t)seg * kSlotVec) + vt;
+      // Not last: publish this segment's partial in slot `order`, tagged
+      // with the segment, then count it.
+      if (tid == 0)
+        __hip_atomic_store(s.tags + t * kSkSlots + order, seg, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      f32x4_t* const dst = reinterpret_cast<f32x4_t*>(
+                               s.slots + ((int64_t)t * kSkSlots + order) * kSlotVec) + vt;
 #pragma unroll
       for (int a = 0; a < 8; ++a)
 #pragma unroll
@@ -1027,6 +1039,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
              ++polls < kSkSpinLimit)
         __builtin_amdgcn_s_sleep(2);
       *arrival = polls < kSkSpinLimit;
+      // which segment each stored slot holds (written before it was counted)
+      arrival[1] = __hip_atomic_load(s.tags + t * kSkSlots, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
       if (polls >= kSkSpinLimit) {
         __hip_atomic_store(s.status, 1 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1034,16 +1049,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
       }
     }
     __syncthreads();
-    const bool complete = *arrival;
-    __syncthreads();  // the word is staged output space below
+    const bool complete = arrival[0];
+    const int tag0 = arrival[1];
+    __syncthreads();  // the words are staged output space below
     if (!complete) continue;
-    // The (one or two) other segments, in segment order: o1 < o2.
+    // The slots of the (one or two) other segments in segment order: the
+    // lower one, o1, and the higher (with one stored partial it is slot 0).
     const int o1 = seg == 0 ? 1 : 0;
-    const int o2 = seg == 2 ? 1 : 2;
+    const int slot1 = tag0 == o1 ? 0 : 1, slot2 = 1 - slot1;
     const f32x4_t* const tbase =
-        reinterpret_cast<const f32x4_t*>(s.slots + (int64_t)t * kSkMaxSeg * kSlotVec) + vt;
-    const f32x4_t* const src1 = tbase + (int64_t)o1 * kSlotVec;
-    const f32x4_t* const src2 = tbase + (int64_t)o2 * kSlotVec;
+        reinterpret_cast<const f32x4_t*>(s.slots + (int64_t)t * kSkSlots * kSlotVec) + vt;
+    const f32x4_t* const src1 = tbase + (int64_t)(nseg == 2 ? 0 : slot1) * kSlotVec;
+    const f32x4_t* const src2 = tbase + (int64_t)slot2 * kSlotVec;
     // One accumulator row (a) at a time: load its partials (loads and wait in
     // one asm statement, so its outputs are complete when it returns), sum
     // each block in segment order -- fp32 add is commutative, so putting this
@@ -1693,7 +1710,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   pl.KT = (int)KT;
   pl.ks = (int)ks;
   pl.counter_bytes = kSkCounterBytes;
-  pl.bytes = pl.counter_bytes + T * kSkMaxSeg * kSlotVec * (int64_t)sizeof(f32x4_t);
+  pl.bytes = pl.counter_bytes + T * kSkSlots * kSlotVec * (int64_t)sizeof(f32x4_t);
   return pl;
 }
 
@@ -1705,9 +1722,11 @@ int launch_gemm_sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
   // whole tile columns, m fastest: down_proj at M = 3100 ran 266-269 us
   // against 280-282 us with groups of four tile rows (one process)
   g.gm = g.tiles_m;
-  SkArgs s{static_cast<int*>(ws), reinterpret_cast<int*>(static_cast<char*>(ws) + kSkStatusOffset),
-           reinterpret_cast<f32x4_t*>(static_cast<char*>(ws) + pl.counter_bytes), (int)pl.tiles,
-           pl.KT, pl.ks, pl.G};
+  char* const base = static_cast<char*>(ws);
+  SkArgs s{reinterpret_cast<int*>(base), reinterpret_cast<int*>(base + kSkStatusOffset),
+           reinterpret_cast<int*>(base + kSkTagOffset),
+           reinterpret_cast<f32x4_t*>(base + pl.counter_bytes), (int)pl.tiles, pl.KT, pl.ks,
+           pl.G};
   const int64_t grid = ((pl.G + 7) / 8) * 8;
   hipLaunchKernelGGL((gemm_sk_kernel<ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st, g, s);
   return launch_status();
