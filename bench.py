@@ -18,6 +18,8 @@ the BASELINE shapes, every kernel launched once through the C ABI:
                    prefill.
   down_proj_vendor the same GEMM on the vendor BLAS (F.linear, hipBLASLt),
                    measured beside it for that per-site choice.
+  q_proj_vendor    q_proj on the vendor BLAS, which the fused path keeps
+                   for q/o (this library's linear only ties it there).
 
 Inputs are resident in HBM before timing.  Each HBM-bound kernel rotates
 over its own ring of input sets (and keeps its outputs alive for one ring
@@ -189,6 +191,9 @@ def build_workload():
          (M * H + 2 * FF * H + M * FF) * b2, 2 * 2 * M * FF * H, "mfma"),
         ("down_proj", lambda i: linear.linear_hip(*pick(down, i)),
          (M * FF + H * FF + M * H) * b2, 2 * M * H * FF, "mfma"),
+        # the q/o projection on the vendor BLAS, which the fused path keeps for it
+        ("q_proj_vendor", lambda i: torch.nn.functional.linear(pick(proj, i)[0], pick(proj, i)[1]),
+         (M * H + H * H + M * H) * b2, 2 * M * H * H, "mfma"),
         ("down_proj_vendor", lambda i: torch.nn.functional.linear(*pick(down, i)),
          (M * FF + H * FF + M * H) * b2, 2 * M * H * FF, "mfma"),
     ]
@@ -196,7 +201,8 @@ def build_workload():
              "add_layernorm": len(addln_xr), "rope_text": len(rope_qk),
              "rope_vision": len(rope_qkv), "qk_norm_rope": len(rope_qk),
              "qk_norm_rope_unfused": len(rope_qk), "q_proj": len(proj), "o_proj": len(proj),
-             "gate_silu_mul": len(p5), "down_proj": len(down), "down_proj_vendor": len(down)}
+             "gate_silu_mul": len(p5), "down_proj": len(down), "q_proj_vendor": len(proj),
+             "down_proj_vendor": len(down)}
     spacer = lambda: fused_ffn.gate_silu_mul_hip(p5[0][0], p5[0][1].t(), p5[0][2].t())  # noqa: E731
     return ents, rings, spacer
 
@@ -1176,7 +1182,7 @@ def main() -> int:
     hbm = [kern[n] for n in VALUE_SITES]
     agg = sum(k["bytes"] for k in hbm) / (sum(k["us"] for k in hbm) * 1e-6) / 1e9
     mlp_ms = (kern["gate_silu_mul"]["us"] + kern["down_proj"]["us"]) / 1e3
-    dom_name = max((n for n in kern if n != "down_proj_vendor"), key=lambda n: kern[n]["us"])
+    dom_name = max((n for n in kern if not n.endswith("_vendor")), key=lambda n: kern[n]["us"])
     dom = kern[dom_name]
     if dom["bound"] == "hbm":
         roof = {"kernel": dom_name, "bound": "hbm", "achieved": dom["gbps"], "peak": HBM_PEAK_GBS,
@@ -1224,7 +1230,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(sum(v["us"] for n, v in kern.items() if n != "down_proj_vendor")
+        "ms_per_step": round(sum(v["us"] for n, v in kern.items() if not n.endswith("_vendor"))
                              / 1e3, 3),
         "wall_ms_per_step": round(wall / K * 1e3, 3),
         "higher_is_better": True,
