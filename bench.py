@@ -12,7 +12,7 @@ the BASELINE shapes, every kernel launched once through the C ABI:
   q_proj, o_proj   [3100,4096] x [4096,4096]^T      (config 3)
   gate_silu_mul    [3100,4096] x 2 x [12288,4096]^T (config 3, P5)
   down_proj        [3100,12288] x [4096,12288]^T on this library's linear
-                   (208 output tiles: the data-parallel four-wave kernel),
+                   (208 output tiles: the four-wave stream-K schedule),
                    which the fused MLP uses for this shape (the reference
                    keeps the vendor BLAS); with P5 it makes the LM MLP
                    prefill.

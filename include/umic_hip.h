@@ -241,9 +241,11 @@ int umic_linear_bf16(const void* x, const void* w, const void* bias, void* out,
  * Bytes of device workspace umic_linear_ws_bf16 uses for this shape on the
  * current device: nonzero when the output's 256 x 256 tiles leave enough of
  * the device's CUs idle and the K loop is long (then a stream-K schedule
- * spreads the K loop over every CU; with K % 64 == 0, at most 11/16 of the
- * CUs' count in tiles, as the data-parallel kernel is faster beyond), 0 when
- * the data-parallel kernel is used and no workspace is needed.
+ * spreads the K loop over the idle CUs too: for few tiles, and with
+ * K % 64 == 0 up to 11/16 of the CUs' count in tiles, over up to twice as
+ * many workgroups; beyond that, with K % 64 == 0 and K >= 8192, the K loop
+ * tails of every tile over the CUs the tiles leave idle), 0 when the
+ * data-parallel kernel is used and no workspace is needed.
  * Host-only query; enqueues nothing.
  */
 int64_t umic_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
@@ -277,12 +279,13 @@ int umic_linear_ws_bf16(const void* x, const void* w, const void* bias, void* ou
  * numerics, shape rules and results as umic_linear_ws_bf16 with a large
  * enough workspace; shapes the data-parallel kernel or the GEMV serve run
  * those, as there.  A shape whose stream-K workspace
- * (umic_linear_workspace_bytes) exceeds 64 MiB -- more than 127 output
- * tiles of 256 x 256 -- returns UMIC_ERR_SCRATCH before any launch.  At
- * N = 4096, K = 12288 (the MLP down projection) that admits M <= 1792; M
- * from 1793 to 2816 (stream-K, over 64 MiB) needs umic_linear_ws_bf16, and the
- * BASELINE prefill (M = 3100, 208 tiles) runs the data-parallel kernel
- * here too.  The device's first call clears the scratch's
+ * (umic_linear_workspace_bytes) exceeds 64 MiB -- the schedule for
+ * fewer tiles with more than 127 output tiles of 256 x 256 -- returns
+ * UMIC_ERR_SCRATCH before any launch.  At N = 4096, K = 12288 (the MLP
+ * down projection) that admits M <= 1792 and, on the schedule for tiles
+ * that fill most CUs (which always fits), M from 2817 to 3968, the BASELINE
+ * prefill (M = 3100, 208 tiles, 63.8 MiB) included; M from 1793 to 2816
+ * needs umic_linear_ws_bf16.  The device's first call clears the scratch's
  * counter region with a kernel (no memset); every launch leaves it cleared.
  * All calls on one device share its scratch: calls that may overlap in time
  * on one device (different streams without ordering) may give wrong

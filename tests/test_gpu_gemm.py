@@ -160,6 +160,66 @@ def test_stream_k_deterministic_and_close_to_data_parallel():
     assert ((y1.float() - ydp.float()).abs().max() / ydp.float().abs().max()).item() <= 2.0 ** -7
 
 
+# Shapes with K % 64 == 0 and K >= 8192 whose tiles fill more than 11/16 of
+# the CUs but leave some idle take the four-wave stream-K schedule (tails of
+# every tile on the idle CUs, one or two pieces per tile, the main workgroup
+# reducing): down_proj and K = 8192 at M = 3100 (208 tiles; 2-piece tiles
+# and the 28-row last tile row), and a shape whose tail pieces end on tile
+# boundaries (192 tiles, 64 tails of exactly three tiles' tails).
+W4SK_SHAPES = [(3100, 4096, 12288), (3100, 4096, 8192), (2900, 4096, 8192)]
+
+
+def _dp_linear(x, w, b=None, act=0):
+    from umic import _lib
+
+    M, K = x.shape
+    N = w.shape[0]
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    _lib.call("umic_linear_bf16", x.data_ptr(), w.data_ptr(), _lib.ptr(b), y.data_ptr(), M, N, K,
+              K, K, N, act, _lib.stream_of(x))
+    return y
+
+
+@pytest.mark.parametrize("M,N,K", W4SK_SHAPES)
+def test_four_wave_stream_k_close_to_data_parallel(M, N, K):
+    """Bit-reproducible, within fp32 summation-order noise of the
+    data-parallel kernel (itself checked against the oracle), and within the
+    GEMM tolerance of fp32 torch."""
+    assert _sk_bytes(M, N, K) > 0
+    print(f"four-wave stream-K M={M} N={N} K={K}", flush=True)
+    torch.manual_seed(M + K)
+    x = torch.randn(M, K).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K) * 0.02).to(torch.bfloat16).to(DEV)
+    y1 = linear.linear_hip(x, w)
+    y2 = linear.linear_hip(x, w)
+    ydp = _dp_linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    d = ulp(bits(y1), bits(ydp))
+    assert (d <= 1).mean() > 0.999, np.bincount(d.ravel())[:8]
+    assert ((y1.float() - ydp.float()).abs().max() / ydp.float().abs().max()).item() <= 2.0 ** -7
+    ref = x.float() @ w.float().t()
+    assert max_rel_err(y1, ref) <= TOL
+
+
+@pytest.mark.parametrize("act,code", [("gelu", 1), ("gelu_tanh", 2)])
+def test_four_wave_stream_k_bias_gelu(act, code):
+    """The bias + GELU epilogue after the partial sums, against the
+    data-parallel kernel's."""
+    M, N, K = 3100, 4096, 8192
+    assert _sk_bytes(M, N, K) > 0
+    print(f"four-wave stream-K epilogue {act}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    x = bf16_randn(M, K, gen=g).to(DEV)
+    w = bf16_randn(N, K, scale=0.02, gen=g).to(DEV)
+    b = bf16_randn(N, scale=0.5, gen=g).to(DEV)
+    y = linear.linear_hip(x, w, b, act=act)
+    ydp = _dp_linear(x, w, b, code)
+    torch.cuda.synchronize()
+    d = ulp(bits(y), bits(ydp))
+    assert (d <= 1).mean() > 0.999, np.bincount(d.ravel())[:8]
+
+
 def test_stream_k_workspace_shared_across_shapes():
     """One stream's workspace serves stream-K calls of any shape in turn: the
     tile counters sit in a fixed region ahead of every call's partial slots,
@@ -185,12 +245,12 @@ def test_stream_k_workspace_shared_across_shapes():
 
 
 def test_down_proj_full_shape_vs_fp32():
-    """BASELINE config 3 down_proj (208 tiles: the data-parallel kernel on the
-    four-wave core, stream-K planning none) against fp32 torch."""
+    """BASELINE config 3 down_proj (208 tiles: the four-wave stream-K
+    schedule) against fp32 torch."""
     torch.manual_seed(6)
     x = torch.randn(3100, 12288).to(torch.bfloat16).to(DEV)
     w = (torch.randn(4096, 12288) * 0.02).to(torch.bfloat16).to(DEV)
-    assert _sk_bytes(3100, 4096, 12288) == 0
+    assert _sk_bytes(3100, 4096, 12288) > 0
     y = linear.linear_hip(x, w)
     ref = x.float() @ w.float().t()
     assert max_rel_err(y, ref) <= TOL and rel_err(y, ref) <= TOL

@@ -64,3 +64,41 @@ def test_wait_gives_up_on_a_corrupted_counter():
     torch.cuda.synchronize()
     assert int(status.item()) == 0 and not counters.any()
     assert torch.equal(out2, ref)
+
+
+def test_four_wave_wait_gives_up_on_a_corrupted_counter():
+    """The four-wave schedule (M = 3100, K = 8192, 208 tiles): its main
+    workgroups wait for their tiles' tail pieces on counters[t]; tile 0's
+    preset far past any count the launch produces makes its wait give up."""
+    M, N, K = 3100, 4096, 8192
+    need = _lib.lib().umic_linear_workspace_bytes(M, N, K)
+    print(f"four-wave stream-K bounded wait M={M} N={N} K={K} ws={need}", flush=True)
+    assert need > STATUS_OFFSET + 4
+    g = torch.Generator().manual_seed(12)
+    x = bf16_randn(M, K, gen=g).to(DEV)
+    w = bf16_randn(N, K, scale=0.02, gen=g).to(DEV)
+    clean_ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    _call(x, w, ref, clean_ws)
+
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    counters = ws[:STATUS_OFFSET].view(torch.int32)   # pieces stored, per tile
+    status = ws[STATUS_OFFSET:STATUS_OFFSET + 4].view(torch.int32)
+    counters[0] = 1000                                 # tile 0's count
+    sentinel = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = sentinel.clone()
+    _call(x, w, out, ws)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1                     # tile 0 gave up
+    assert not counters.any()                          # counters reset
+    # tile 0 is the output block rows 0..255, columns 0..255
+    assert torch.equal(out[:256, :256], sentinel[:256, :256])
+    assert torch.equal(out[256:], ref[256:]) and torch.equal(out[:, 256:], ref[:, 256:])
+    assert int(clean_ws[STATUS_OFFSET:STATUS_OFFSET + 4].view(torch.int32).item()) == 0
+
+    status.zero_()
+    out2 = torch.empty_like(out)
+    _call(x, w, out2, ws)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0 and not counters.any()
+    assert torch.equal(out2, ref)

@@ -3,9 +3,10 @@ static scratch (no workspace argument, no allocation).
 
 Through the C ABI, against umic_linear_ws_bf16 on a caller workspace (the
 same kernel, so bit for bit): stream-K calls in a row on one stream, each
-smaller than the one before (the first, 96 tiles, near the scratch's
-limit; the last with a bias and the GELU epilogue), so each runs on the
-scratch the previous left behind; a few-row (GEMV) and a data-parallel
+smaller than the one before (the BASELINE down_proj on the four-wave
+schedule, 63.8 MiB; then 96 tiles of the eight-wave one; the last with a
+bias and the GELU epilogue), so each runs on the scratch the previous left
+behind; a few-row (GEMV) and a data-parallel
 shape, which need no scratch and pass through to umic_linear_bf16; and a
 shape whose workspace exceeds the 64 MiB scratch, rejected before any
 launch.
@@ -54,7 +55,8 @@ def _with_workspace(x, w, b, act):
 
 
 def test_static_scratch_matches_the_workspace_entry_point():
-    calls = [((1536, 4096, 12288), 1, False, _lib.UMIC_ACT_NONE),
+    calls = [((3100, 4096, 12288), 7, False, _lib.UMIC_ACT_NONE),
+             ((1536, 4096, 12288), 1, False, _lib.UMIC_ACT_NONE),
              ((300, 4096, 12288), 6, False, _lib.UMIC_ACT_NONE),
              ((32, 2048, 12288), 2, True, _lib.UMIC_ACT_GELU)]
     for (M, N, K), seed, bias, act in calls:

@@ -587,6 +587,7 @@ struct W4Tile {
   int xbase;         // first x row of this wave's fragments
   W4Src src;         // the tile being loaded
   int xstep, wstep;  // bytes between 8-row load groups (wave-uniform)
+  int kbase;         // first K element of the segment the K loop runs
   f32x4_t acc[8][8];
   bf16x8_t fa[2][8], fb[2][8];
 
@@ -604,6 +605,7 @@ struct W4Tile {
     fo0 = frow * kW4Row + ((fch ^ w4_swz(frow)) * 16);
     fo1 = frow * kW4Row + (((4 + fch) ^ w4_swz(frow)) * 16);
     xbase = wm * 128;  // wave pair wm takes x rows [wm * 128, ...) of the tile
+    kbase = 0;
     const bool up = NB == 2 && wave >= 2;
     xstep = __builtin_amdgcn_readfirstlane((int)(8 * g.ldx * 2));
     wstep = __builtin_amdgcn_readfirstlane((int)(8 * (up ? g.ldw1 : g.ldw0) * 2));
@@ -653,7 +655,9 @@ struct W4Tile {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r.rx, (lds_void*)d, 16, (q & 1) ? r.xoff1 : r.xoff0,
                                                k * 2 + (q & 7) * xstep, 0, 0);
   }
-  __device__ __forceinline__ void issue(int stage, int k, int q) { issue(src, stage, k, q); }
+  __device__ __forceinline__ void issue(int stage, int k, int q) {
+    issue(src, stage, kbase + k, q);
+  }
 
   // Fragment f (0..7: weight blocks, 8..15: x blocks) of K half h of a stage.
   __device__ __forceinline__ void read(int buf, int stage, int h, int f) {
@@ -716,74 +720,202 @@ struct W4Tile {
     for (int j = 1; j < n; ++j) stage(j, std::false_type{});
     w4_wait<0, 0>();
     w4_barrier();
-    fence_results();
+    fence_results<NBX>();
   }
 
-  // The MFMA results are read next: 32 wait states, in statements that take
-  // every accumulator, so no read moves above them.
+  // The MFMA results are read next: 32 wait states, then a statement per
+  // live accumulator (blocks b < NBX; the others are never written or read)
+  // that takes it, so no read moves above the wait states -- and no value
+  // of an accumulator the K loop did not write is kept alive (a loop over
+  // tiles of different NBX would otherwise carry them all across its
+  // iterations).
+  template <int NBX>
   __device__ __forceinline__ void fence_results() {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      if (a == 0)
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                     : "+a"(acc[a][0]), "+a"(acc[a][1]), "+a"(acc[a][2]), "+a"(acc[a][3]),
-                       "+a"(acc[a][4]), "+a"(acc[a][5]), "+a"(acc[a][6]), "+a"(acc[a][7]));
-      else
-        asm volatile(""
-                     : "+a"(acc[a][0]), "+a"(acc[a][1]), "+a"(acc[a][2]), "+a"(acc[a][3]),
-                       "+a"(acc[a][4]), "+a"(acc[a][5]), "+a"(acc[a][6]), "+a"(acc[a][7]));
-    }
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int b = 0; b < NBX; ++b) asm volatile("" : "+a"(acc[a][b]));
   }
 
   static constexpr int kOutCols = NB == 1 ? kBW : kBW / 2;
   static constexpr int kOutRow = kOutCols * 2 + 16;  // staged bytes per output row
   static_assert(kBM * kOutRow <= kW4LdsBytes, "staged tile must fit the LDS");
 
-  // Stage the tile's live fragments as bf16 rows in LDS (bias, GELU or
-  // silu(g) * u in fp32, one rounding), as gemm_kernel's epilogue.
+  // The linear's bias chunk of fragment block a (4 output columns of this lane).
+  template <bool BIAS>
+  __device__ __forceinline__ f32x4_t bias_of(const GemmArgs& g, int n0, int a) const {
+    f32x4_t bias = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (NB == 1 && BIAS) {
+      const int col = arow(a) + fch * 4;
+      if (n0 + col < g.N) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(g.bias + n0 + col);
+        bias[0] = bf_lo(bw.x);
+        bias[1] = bf_hi(bw.x);
+        bias[2] = bf_lo(bw.y);
+        bias[3] = bf_hi(bw.y);
+      }
+    }
+    return bias;
+  }
+
+  // Stage block (a, b) of the output tile, v its fp32 sums (P5: the gate
+  // sums, u the up sums), as bf16 in LDS: bias, GELU or silu(g) * u in fp32,
+  // one rounding, as gemm_kernel's epilogue.
+  template <int ACT, bool BIAS>
+  __device__ __forceinline__ void stage_block(int a, int b, const f32x4_t& v, const f32x4_t& u,
+                                              const f32x4_t& bias) {
+    char* out = (char*)lds;
+    const int col = (NB == 1 ? arow(a) : wn * 64 + a * 16) + fch * 4;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e];
+      if constexpr (NB == 2) {
+        const float den = 1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+        x = x * __builtin_amdgcn_rcpf(den) * u[e];
+      } else {
+        if constexpr (BIAS) x = x + bias[e];
+        if constexpr (ACT == UMIC_ACT_GELU) x = gelu_erf(x);
+        if constexpr (ACT == UMIC_ACT_GELU_TANH) x = gelu_tanh(x);
+      }
+      o[e] = x;
+    }
+    uint2 pk;
+    pk.x = pack2(o[0], o[1]);
+    pk.y = pack2(o[2], o[3]);
+    *reinterpret_cast<uint2*>(out + (xbase + b * 16 + frow) * kOutRow + col * 2) = pk;
+  }
+
+  // Stage the tile's live fragments as bf16 rows in LDS.
   template <int NBX, int ACT, bool BIAS>
   __device__ __forceinline__ void stage_out(const GemmArgs& g, int n0) {
     constexpr int kOutBlocks = NB == 1 ? 8 : 4;
-    char* out = (char*)lds;
 #pragma unroll
     for (int a = 0; a < kOutBlocks; ++a) {
-      const int col = (NB == 1 ? arow(a) : wn * 64 + a * 16) + fch * 4;
-      f32x4_t bias = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (NB == 1 && BIAS) {
-        if (n0 + col < g.N) {
-          const uint2 bw = *reinterpret_cast<const uint2*>(g.bias + n0 + col);
-          bias[0] = bf_lo(bw.x);
-          bias[1] = bf_hi(bw.x);
-          bias[2] = bf_lo(bw.y);
-          bias[3] = bf_hi(bw.y);
-        }
-      }
+      const f32x4_t bias = bias_of<BIAS>(g, n0, a);
 #pragma unroll
       for (int b = 0; b < NBX; ++b) {
-        const f32x4_t v = acc[a][b];
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = v[e];
-          if constexpr (NB == 2) {
-            const float den = 1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
-            x = x * __builtin_amdgcn_rcpf(den) * acc[a + 4][b][e];
-          } else {
-            if constexpr (BIAS) x = x + bias[e];
-            if constexpr (ACT == UMIC_ACT_GELU) x = gelu_erf(x);
-            if constexpr (ACT == UMIC_ACT_GELU_TANH) x = gelu_tanh(x);
-          }
-          o[e] = x;
-        }
-        uint2 pk;
-        pk.x = pack2(o[0], o[1]);
-        pk.y = pack2(o[2], o[3]);
-        *reinterpret_cast<uint2*>(out + (xbase + b * 16 + frow) * kOutRow + col * 2) = pk;
+        stage_block<ACT, BIAS>(a, b, acc[a][b], acc[NB == 2 ? a + 4 : a][b], bias);
         __builtin_amdgcn_sched_barrier(0);  // one block's reads at a time
       }
     }
   }
+
+  // Stream-K partials (linear only).  A lane's share of a partial is its
+  // wave's 64 KB region, [a][b][lane] (block (a, b) at (a * 8 + b) * 64
+  // f32x4 from the lane's base, so four consecutive blocks are reached with
+  // immediate offsets of one address), written and read with device-scope
+  // (sc1) accesses.  Called after fence_results().  A store of more than 8
+  // bytes reads its data registers after issue, and the compiler's hazard
+  // checks do not see into the asm: the s_nop keeps the next instruction
+  // (typically the copy of the next block into the same registers) from
+  // overwriting them first.
+  template <int NBX>
+  __device__ __forceinline__ void store_partial(f32x4_t* p) {
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4_t* const q = p + (a * 8 + h * 4) * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (h * 4 + i < NBX)
+            asm volatile("global_store_dwordx4 %0, %1, off offset:%2 sc1\n\ts_nop 1"
+                         ::"v"(q), "v"(acc[a][h * 4 + i]), "n"(i * 1024) : "memory");
+      }
+  }
+
+  // Stage the tile with its tail partials added: acc (K steps [0, ks)) +
+  // the lower tail piece p1 (+ the higher one, p2, when `two`), summed in
+  // that order.
+  template <int NBX, int ACT, bool BIAS>
+  __device__ __forceinline__ void stage_out_sum(const GemmArgs& g, int n0, const f32x4_t* p1,
+                                                const f32x4_t* p2, bool two) {
+    static_assert(NB == 1, "stream-K runs the linear");
+    if (!two) {
+#pragma unroll
+      for (int a = 0; a < 8; a += 2) {
+        f32x4_t q[16];
+        w4_load16(q, p1 + a * 512, p1 + (a + 1) * 512);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const f32x4_t bias = bias_of<BIAS>(g, n0, a + r);
+#pragma unroll
+          for (int b = 0; b < NBX; ++b) {
+            stage_block<ACT, BIAS>(a + r, b, acc[a + r][b] + q[r * 8 + b], q[0], bias);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        f32x4_t q[16];
+        w4_load16(q, p1 + a * 512, p2 + a * 512);
+        const f32x4_t bias = bias_of<BIAS>(g, n0, a);
+#pragma unroll
+        for (int b = 0; b < NBX; ++b) {
+          stage_block<ACT, BIAS>(a, b, (acc[a][b] + q[b]) + q[8 + b], q[0], bias);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  }
+
+  // Two partial rows (8 blocks each, at u and v), device-scope loads issued
+  // and waited for inside ONE asm statement: the outputs are valid when it
+  // returns (a load left in flight across statements is unsafe: the
+  // compiler may move or spill its destination before the data arrives).
+  static __device__ __forceinline__ void w4_load16(f32x4_t (&q)[16], const f32x4_t* u,
+                                                   const f32x4_t* v) {
+    asm volatile(
+        "global_load_dwordx4 %0, %16, off sc1\n\t"
+        "global_load_dwordx4 %1, %16, off offset:1024 sc1\n\t"
+        "global_load_dwordx4 %2, %16, off offset:2048 sc1\n\t"
+        "global_load_dwordx4 %3, %16, off offset:3072 sc1\n\t"
+        "global_load_dwordx4 %4, %17, off sc1\n\t"
+        "global_load_dwordx4 %5, %17, off offset:1024 sc1\n\t"
+        "global_load_dwordx4 %6, %17, off offset:2048 sc1\n\t"
+        "global_load_dwordx4 %7, %17, off offset:3072 sc1\n\t"
+        "global_load_dwordx4 %8, %18, off sc1\n\t"
+        "global_load_dwordx4 %9, %18, off offset:1024 sc1\n\t"
+        "global_load_dwordx4 %10, %18, off offset:2048 sc1\n\t"
+        "global_load_dwordx4 %11, %18, off offset:3072 sc1\n\t"
+        "global_load_dwordx4 %12, %19, off sc1\n\t"
+        "global_load_dwordx4 %13, %19, off offset:1024 sc1\n\t"
+        "global_load_dwordx4 %14, %19, off offset:2048 sc1\n\t"
+        "global_load_dwordx4 %15, %19, off offset:3072 sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]),
+          "=&v"(q[6]), "=&v"(q[7]), "=&v"(q[8]), "=&v"(q[9]), "=&v"(q[10]), "=&v"(q[11]),
+          "=&v"(q[12]), "=&v"(q[13]), "=&v"(q[14]), "=&v"(q[15])
+        : "v"(u), "v"(u + 256), "v"(v), "v"(v + 256)
+        : "memory");
+  }
 };
+
+// Stream the tile staged in LDS out as whole rows of 16-byte stores (rows
+// [m0, mlim) of the output).
+template <int NB>
+__device__ __forceinline__ void w4_flush(const char* smem, const GemmArgs& g, int m0, int n0,
+                                         int64_t mlim) {
+  constexpr int kOutCols = W4Tile<NB>::kOutCols;
+  constexpr int kOutRow = W4Tile<NB>::kOutRow;
+  constexpr int kChunks = kOutCols / 8;
+  constexpr int kRowsPerPass = kW4Threads / kChunks;
+  const int cc = threadIdx.x % kChunks;
+  const int64_t col = n0 + cc * 8;
+  if (col < g.N) {
+#pragma unroll 4
+    for (int r = threadIdx.x / kChunks; r < kBM; r += kRowsPerPass) {
+      const int64_t m = (int64_t)m0 + r;
+      if (m >= mlim) break;
+      *reinterpret_cast<u32x4*>(g.out + m * g.ldo + col) =
+          *reinterpret_cast<const u32x4*>(smem + r * kOutRow + cc * 16);
+    }
+  }
+}
 
 template <int NB, int NBX, int ACT, bool BIAS>
 __device__ __forceinline__ void w4_tile(W4Tile<NB>& c, const GemmArgs& g, int n, int n0) {
@@ -824,23 +956,8 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm_w4_kernel(GemmArgs g) {
     case 1: w4_tile<NB, 1, ACT, BIAS>(c, g, n, n0); break;
     default: w4_tile<NB, 0, ACT, BIAS>(c, g, n, n0); break;
   }
-  // Stream the staged tile out as whole rows of 16-byte stores.
   __syncthreads();
-  constexpr int kOutCols = W4Tile<NB>::kOutCols;
-  constexpr int kOutRow = W4Tile<NB>::kOutRow;
-  constexpr int kChunks = kOutCols / 8;
-  constexpr int kRowsPerPass = kW4Threads / kChunks;
-  const int cc = threadIdx.x % kChunks;
-  const int64_t col = n0 + cc * 8;
-  if (col < g.N) {
-#pragma unroll 4
-    for (int r = threadIdx.x / kChunks; r < kBM; r += kRowsPerPass) {
-      const int64_t m = (int64_t)m0 + r;
-      if (m >= mlim) break;
-      *reinterpret_cast<u32x4*>(g.out + m * g.ldo + col) =
-          *reinterpret_cast<const u32x4*>(smem + r * kOutRow + cc * 16);
-    }
-  }
+  w4_flush<NB>(smem, g, m0, n0, mlim);
 }
 
 // Stream-K linear, K-aligned.  With T tiles < G workgroups (one per CU),
@@ -1022,7 +1139,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
       for (int a = 0; a < 8; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          asm volatile("global_store_dwordx4 %0, %1, off sc1"
+          asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"  // store-data hazard
                        :: "v"(dst + (a * 4 + b) * kThreads), "v"(p.acc[a][b]) : "memory");
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1094,6 +1211,159 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
       __hip_atomic_store(written, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+// ---- Stream-K on the four-wave core ---------------------------------------
+//
+// For K % 64 == 0 and tiles that fill most but not all CUs (M = 3100 at
+// N = 4096: 208 tiles on 256 CUs), the data-parallel four-wave kernel leaves
+// the remaining CUs idle.  Here Gt "tail" workgroups (a multiple of 8, at
+// most T) take the last L = KT - ks stages of every tile while T "main"
+// workgroups run the first ks stages of one tile each, in lockstep as in the
+// data-parallel kernel.  Tail j owns units [j*Ut/Gt, (j+1)*Ut/Gt) of the
+// Ut = T*L (tile, stage) pairs, tile-major, so with Gt <= T a tile's tail
+// stages are covered by one or two pieces (tails owner(t*L) ..
+// owner(t*L + L - 1)); piece (j, t) stores its fp32 partial in slot j + t
+// (pieces run along the unit line, each step advancing j or t or both, so
+// the slots are distinct: T + Gt - 1 of them) and counts itself on the
+// tile's counter.  The main workgroup always reduces: after its K loop it
+// waits for the tile's piece count, adds the pieces in K order (main, lower
+// piece, higher piece: deterministic whatever the arrival order), applies
+// the epilogue, stores the tile and clears the counter.  Tails take the
+// lowest workgroup ids, which the hardware dispatches first, and never wait,
+// so a waiting main's tails are running or done; the wait is still bounded
+// by kSkSpinLimit polls, recording 1 + tile in the status word on expiry
+// (the tile is then left unwritten and the launch ends normally).
+// Workspace: the stream-K counter region (counters[t] at 4t bytes, the
+// status word at kSkStatusOffset), then the slots, each [wave][a][b][lane]
+// f32x4 (256 KB).
+struct W4SkArgs {
+  int* counters;   // [T]: tail pieces stored (zero between launches)
+  int* status;     // sticky status word (0: every wait completed)
+  f32x4_t* slots;  // [T + Gt - 1][kW4SlotVec]
+  int T, KT, ks, Gt;
+};
+constexpr int kW4SlotVec = 64 * kW4Threads;  // f32x4 per partial (256 KB)
+constexpr int kW4SkFlag = 150 * 1024;        // LDS word past the staged output
+
+// Tail workgroup owning unit v, and tail j's first unit.
+__device__ __forceinline__ int w4sk_owner(int64_t v, int64_t Ut, int Gt) {
+  return (int)(((v + 1) * Gt - 1) / Ut);
+}
+__device__ __forceinline__ int w4sk_start(int j, int64_t Ut, int Gt) {
+  return (int)((int64_t)j * Ut / Gt);
+}
+
+template <int NBX>
+__device__ __forceinline__ void w4sk_piece(W4Tile<1>& c, int n, f32x4_t* dst) {
+  c.template kloop<NBX>(n);
+  c.template store_partial<NBX>(dst);
+}
+
+// The main workgroup's tile: K loop over [0, ks), the wait for its np tail
+// pieces, the reduction and staging.  Returns false when the wait gave up.
+template <int NBX, int ACT, bool BIAS>
+__device__ __forceinline__ bool w4sk_main(W4Tile<1>& c, const GemmArgs& g, const W4SkArgs& s,
+                                          int t, int n0, int np, const f32x4_t* p1,
+                                          const f32x4_t* p2, int* flag) {
+  c.template kloop<NBX>(s.ks);
+  if (threadIdx.x == 0) {
+    int* const cnt = s.counters + t;
+    int polls = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != np &&
+           ++polls < kSkSpinLimit)
+      __builtin_amdgcn_s_sleep(2);
+    *flag = polls < kSkSpinLimit;
+    if (polls >= kSkSpinLimit)
+      __hip_atomic_store(s.status, 1 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!*flag) return false;
+  c.template stage_out_sum<NBX, ACT, BIAS>(g, n0, p1, p2, np == 2);
+  return true;
+}
+
+template <int ACT, bool BIAS>
+__global__ __launch_bounds__(kW4Threads, 1) void gemm_w4sk_kernel(GemmArgs g, W4SkArgs s) {
+  __shared__ __attribute__((aligned(16))) char smem[kW4LdsBytes];
+  const int h = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int L = s.KT - s.ks;
+  const int64_t Ut = (int64_t)s.T * L;
+  W4Tile<1> c;
+  c.init(smem, g);
+  auto begin = [&](int t, int k0, int& m0, int& n0, int64_t& mlim) {
+    tile_origin(g, t, kBW, m0, n0);
+    mlim = std::min<int64_t>(g.M, (int64_t)m0 + g.bm);
+    c.src = c.bind(g, m0, n0, mlim);
+    c.kbase = k0 * kW4BK;
+    const int live = (int)(mlim - m0) - c.xbase;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) c.issue(0, 0, q);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) c.issue(1, kW4BK, q);
+    w4_wait<16, 0>();
+    w4_barrier();
+    return __builtin_amdgcn_readfirstlane(live <= 0 ? 0 : min(8, (live + 15) / 16));
+  };
+  if (h < s.Gt) {
+    // Tail h: its pieces in unit order.
+    for (int v = w4sk_start(h, Ut, s.Gt), vend = w4sk_start(h + 1, Ut, s.Gt); v < vend;) {
+      const int t = v / L, r = v - t * L, len = min(L - r, vend - v);
+      int m0, n0;
+      int64_t mlim;
+      const int nbx = begin(t, s.ks + r, m0, n0, mlim);
+      f32x4_t* const dst = s.slots + (int64_t)(h + t) * kW4SlotVec + c.wave * 4096 + lane;
+      switch (nbx) {
+        case 8: w4sk_piece<8>(c, len, dst); break;
+        case 7: w4sk_piece<7>(c, len, dst); break;
+        case 6: w4sk_piece<6>(c, len, dst); break;
+        case 5: w4sk_piece<5>(c, len, dst); break;
+        case 4: w4sk_piece<4>(c, len, dst); break;
+        case 3: w4sk_piece<3>(c, len, dst); break;
+        case 2: w4sk_piece<2>(c, len, dst); break;
+        case 1: w4sk_piece<1>(c, len, dst); break;
+        default: w4sk_piece<0>(c, len, dst); break;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(s.counters + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v += len;
+    }
+    return;
+  }
+  // Main workgroup u: tile t in the XCD-grouped order (Gt % 8 == 0, so u
+  // and h share their XCD).
+  const int u = h - s.Gt;
+  const int per_xcd = (s.T + 7) >> 3;
+  const int t = (u & 7) * per_xcd + (u >> 3);
+  if (t >= s.T) return;
+  int m0, n0;
+  int64_t mlim;
+  const int nbx = begin(t, 0, m0, n0, mlim);
+  const int j0 = w4sk_owner((int64_t)t * L, Ut, s.Gt);
+  const int j1 = w4sk_owner((int64_t)t * L + L - 1, Ut, s.Gt);
+  const int np = j1 - j0 + 1;
+  const f32x4_t* const p1 = s.slots + (int64_t)(j0 + t) * kW4SlotVec + c.wave * 4096 + lane;
+  const f32x4_t* const p2 = s.slots + (int64_t)(j1 + t) * kW4SlotVec + c.wave * 4096 + lane;
+  int* const flag = reinterpret_cast<int*>(smem + kW4SkFlag);
+  bool ok;
+  switch (nbx) {
+    case 8: ok = w4sk_main<8, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 7: ok = w4sk_main<7, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 6: ok = w4sk_main<6, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 5: ok = w4sk_main<5, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 4: ok = w4sk_main<4, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 3: ok = w4sk_main<3, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 2: ok = w4sk_main<2, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    case 1: ok = w4sk_main<1, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+    default: ok = w4sk_main<0, ACT, BIAS>(c, g, s, t, n0, np, p1, p2, flag); break;
+  }
+  if (!ok) return;
+  __syncthreads();
+  w4_flush<1>(smem, g, m0, n0, mlim);
 }
 
 // ---- Few-row (decode) path --------------------------------------------
@@ -1678,7 +1948,45 @@ struct SkPlan {
   int64_t tiles;
   int G, KT, ks;
   int64_t counter_bytes, bytes;
+  int kind;  // 1: the eight-wave schedule (gemm_sk_kernel), 2: the four-wave one
+  int Gt;    // four-wave: tail workgroups
 };
+
+// The four-wave schedule (gemm_w4sk_kernel) for K % 64 == 0 shapes whose T
+// tiles fill more than kSkMaxTileShare16 / 16 of the CUs but leave some
+// idle, with a long K loop: Gt = min(T, CUs - T rounded up to 8), rounded
+// down to a multiple of 8, tail workgroups, and the main segment ks (stages
+// of 64) the even share T*KT/(T + Gt) plus kW4SkTailExtra stages for the
+// tails' per-piece prologues and partial stores.  Measured on MI355X at
+// M = 3100, N = 4096, in one process against the data-parallel four-wave
+// kernel: down_proj (K = 12288, 208 tiles, Gt = 48) 228-234 against 234-242
+// us over ks = 160..165 (157: no gain, 170+: slower); q/o (K = 4096)
+// 95-99 against 87-89 us at every ks tried -- the partials' stores and the
+// main workgroup's device-scope reads cost more than the idle CUs return,
+// so the schedule needs kW4SkMinKT stages.
+constexpr int kW4SkTailExtra = 4;
+constexpr int kW4SkMinKT = 128;  // K >= 8192
+constexpr int kW4SkMinTail = 4;  // tail stages per tile, at least
+
+SkPlan w4sk_plan(int64_t T, int64_t K, int64_t cus) {
+  SkPlan pl{0, 0, 0, 0, 0, 0, 0, 0};
+  const int64_t KT = K / kW4BK;
+  const int64_t T8 = (T + 7) / 8 * 8;
+  const int64_t Gt = std::min<int64_t>(T, cus - T8) / 8 * 8;
+  if (KT < kW4SkMinKT || Gt < 8 || T > kSkMaxTiles || T * KT >= ((int64_t)1 << 31) / 8)
+    return pl;
+  const int64_t ks = (T * KT + (T + Gt) / 2) / (T + Gt) + kW4SkTailExtra;
+  if (KT - ks < kW4SkMinTail) return pl;
+  pl.tiles = T;
+  pl.G = (int)(Gt + T8);
+  pl.Gt = (int)Gt;
+  pl.KT = (int)KT;
+  pl.ks = (int)ks;
+  pl.kind = 2;
+  pl.counter_bytes = kSkCounterBytes;
+  pl.bytes = kSkCounterBytes + (T + Gt - 1) * kW4SlotVec * (int64_t)sizeof(f32x4_t);
+  return pl;
+}
 
 // Workspace layout and grid of the stream-K launch for this shape, or
 // bytes = 0 when the data-parallel kernel is the better (or only) choice.
@@ -1687,7 +1995,7 @@ struct SkPlan {
 // at most kSkMaxSeg = 3 segments (main, two tail pieces); every workgroup
 // keeps at least kSkMinSteps steps.
 SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
-  SkPlan pl{0, 0, 0, 0, 0, 0};
+  SkPlan pl{0, 0, 0, 0, 0, 0, 0, 0};
   if (M <= kGemvMaxRows || N <= 0 || K <= 0 || K % kBK) return pl;  // few rows: the GEMV
   const int64_t cus = device_cus();
   const int64_t T = ((M + kBM - 1) / kBM) * ((N + kBW - 1) / kBW);
@@ -1695,7 +2003,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   const int64_t G = std::min<int64_t>(cus, 2 * T - 1);
   if (cus <= 0 || G <= T || T * KT * G >= ((int64_t)1 << 31)) return pl;
   if (T > kSkMaxTiles) return pl;
-  if (K % kW4BK == 0 && T * 16 > cus * kSkMaxTileShare16) return pl;
+  if (K % kW4BK == 0 && T * 16 > cus * kSkMaxTileShare16) return w4sk_plan(T, K, cus);
   // Main workgroups take a sixth of the tail beyond the even share, which
   // offsets the tail workgroups' extra segment prologues and partial stores
   // and makes a main workgroup usually the last to arrive at its tile.
@@ -1711,6 +2019,7 @@ SkPlan sk_plan(int64_t M, int64_t N, int64_t K) {
   pl.ks = (int)ks;
   pl.counter_bytes = kSkCounterBytes;
   pl.bytes = pl.counter_bytes + T * kSkSlots * kSlotVec * (int64_t)sizeof(f32x4_t);
+  pl.kind = 1;
   return pl;
 }
 
@@ -1730,6 +2039,27 @@ int launch_gemm_sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
   const int64_t grid = ((pl.G + 7) / 8) * 8;
   hipLaunchKernelGGL((gemm_sk_kernel<ACT, BIAS>), dim3((unsigned)grid), dim3(kThreads), 0, st, g, s);
   return launch_status();
+}
+
+template <int ACT, bool BIAS>
+int launch_gemm_w4sk(GemmArgs g, const SkPlan& pl, void* ws, hipStream_t st) {
+  g.tiles_m = (int)((g.M + kBM - 1) / kBM);
+  g.tiles = (int)pl.tiles;
+  g.bm = kBM;
+  g.gm = kGroupMOne;
+  char* const base = static_cast<char*>(ws);
+  W4SkArgs s{reinterpret_cast<int*>(base), reinterpret_cast<int*>(base + kSkStatusOffset),
+             reinterpret_cast<f32x4_t*>(base + pl.counter_bytes), (int)pl.tiles, pl.KT, pl.ks,
+             pl.Gt};
+  hipLaunchKernelGGL((gemm_w4sk_kernel<ACT, BIAS>), dim3((unsigned)pl.G), dim3(kW4Threads), 0, st,
+                     g, s);
+  return launch_status();
+}
+
+template <int ACT, bool BIAS>
+int launch_sk(const GemmArgs& g, const SkPlan& pl, void* ws, hipStream_t st) {
+  return pl.kind == 2 ? launch_gemm_w4sk<ACT, BIAS>(g, pl, ws, st)
+                      : launch_gemm_sk<ACT, BIAS>(g, pl, ws, st);
 }
 
 // Buffer-resource offsets are 32-bit: every operand (rows x leading dim),
@@ -1845,13 +2175,13 @@ int run_linear_sk(const void* x, const void* w, const void* bias, void* out, int
   GemmArgs g{(const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)w, (const uint16_t*)bias,
              (uint16_t*)out, M, N, K, ldx, ldw, ldw, ldo, 0, 0};
   if (act == UMIC_ACT_GELU)
-    return bias ? launch_gemm_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
-                : launch_gemm_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
+    return bias ? launch_sk<UMIC_ACT_GELU, true>(g, pl, workspace, st)
+                : launch_sk<UMIC_ACT_GELU, false>(g, pl, workspace, st);
   if (act == UMIC_ACT_GELU_TANH)
-    return bias ? launch_gemm_sk<UMIC_ACT_GELU_TANH, true>(g, pl, workspace, st)
-                : launch_gemm_sk<UMIC_ACT_GELU_TANH, false>(g, pl, workspace, st);
-  return bias ? launch_gemm_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
-              : launch_gemm_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
+    return bias ? launch_sk<UMIC_ACT_GELU_TANH, true>(g, pl, workspace, st)
+                : launch_sk<UMIC_ACT_GELU_TANH, false>(g, pl, workspace, st);
+  return bias ? launch_sk<UMIC_ACT_NONE, true>(g, pl, workspace, st)
+              : launch_sk<UMIC_ACT_NONE, false>(g, pl, workspace, st);
 }
 
 }  // namespace

@@ -85,9 +85,11 @@ GEMV_ROWS_DOWN = 2    # the MLP's down projection (and its residual epilogue)
 #     M = 64: 1.45, 256: 0.91, 512: 0.82, 1024: 0.88, 2048: 0.78, 3100: 0.82, 4096: 0.91
 #   ViT fc1 + bias + tanh GELU (K = 1280, N = 5120) vs F.linear then F.gelu:
 #     M = 256: 1.86, 1024: 1.36, 2048: 0.98, 4096: 1.00, 8192: 0.90, 16384: 0.91
-#   down_proj linear (K = 12288, N = 4096; stream-K up to 2816 rows):
-#     M = 64: 3.71, 512: 2.01, 1024: 1.46, 2048: 1.16, 2816: 1.17, 2900: 1.12,
-#     3000: 1.17, 3100: 0.88, 3300: 0.98, 3500: 1.03, 3800: 1.03, 4096: 1.07
+#   down_proj linear (K = 12288, N = 4096; stream-K up to 2816 rows, then
+#   the four-wave stream-K schedule to 3968):
+#     M = 64: 3.71, 512: 2.01, 1024: 1.46, 2048: 1.13, 2816: 1.14, 2900: 1.03,
+#     3000: 1.04, 3100: 0.89, 3300: 0.94, 3500: 1.06, 3800: 1.07, 3968: 1.05,
+#     4096: 1.06
 #   plain q/o_proj linear (K = N = 4096):
 #     M = 64: 5.1, 256: 4.1, 1024: 2.05, 2048: 1.37, 2900: 1.06, 3000: 1.07,
 #     3100: 1.00, 3300: 1.04, 3500: 1.05, 3800: 0.98, 4096: 1.10, 8192: 1.10;
@@ -145,8 +147,10 @@ INEFFICIENT_LINEAR_NAMES = ("q_proj", "o_proj")
 # Per-site choice for the P5 MLP's down_proj, which the reference leaves on
 # the vendor BLAS (integrate.py:80-90, measured a loser on Thor): on MI355X
 # this library's linear beats hipBLASLt in the TILED_MIN_ROWS_DOWN ..
-# TILED_MAX_ROWS_DOWN band (M = 3100: 257 vs 291 us graph-timed), so the
-# fused MLP uses it there and the vendor module for every other row count.
+# TILED_MAX_ROWS_DOWN band (graph-timed, one process, the four-wave stream-K
+# schedule: M = 3100 236.7 against 313.7 us, M = 3300 268.6 against 286.9),
+# so the fused MLP uses it there and the vendor module for every other row
+# count.
 DOWN_PROJ_TILED = True
 
 # ViT projection site list kept from the reference (integrate.py:95); not
