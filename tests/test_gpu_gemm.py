@@ -164,9 +164,10 @@ def test_stream_k_deterministic_and_close_to_data_parallel():
 # the CUs but leave some idle take the four-wave stream-K schedule (tails of
 # every tile on the idle CUs, one or two pieces per tile, the main workgroup
 # reducing): down_proj and K = 8192 at M = 3100 (208 tiles; 2-piece tiles
-# and the 28-row last tile row), and a shape whose tail pieces end on tile
-# boundaries (192 tiles, 64 tails of exactly three tiles' tails).
-W4SK_SHAPES = [(3100, 4096, 12288), (3100, 4096, 8192), (2900, 4096, 8192)]
+# and the 28-row last tile row), a shape whose tail pieces end on tile
+# boundaries (192 tiles, 64 tails of exactly three tiles' tails), and ragged
+# M and N (a last tile column of 160 weight rows).
+W4SK_SHAPES = [(3100, 4096, 12288), (3100, 4096, 8192), (2900, 4096, 8192), (3000, 4000, 8192)]
 
 
 def _dp_linear(x, w, b=None, act=0):
