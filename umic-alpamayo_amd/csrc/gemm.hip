@@ -1934,12 +1934,14 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
 // reduction's device-scope loads, extra prologues), measured on MI355X, so
 // the main segment must be at least kSkMinMain steps (q/o at K = 4096 stays
 // data-parallel; down_proj at K = 12288 gains ~10%); every tail workgroup
-// keeps at least kSkMinSteps steps.  Stream-K runs on the eight-wave core,
-// the data-parallel kernel on the faster four-wave core (K % 64 == 0), so a
-// shape whose tiles already fill most CUs stays data-parallel: at N = 4096,
-// K = 12288 (MI355X, 256 CUs, us data-parallel / stream-K) M = 512 (32
-// tiles): 263 / 169, 2048 (128): 270 / 219, 2560 (160): 274 / 250, 2816
-// (176): 279 / 267, 3100 (208): 252 / 269 -- stream-K up to 11/16 of the CUs.
+// keeps at least kSkMinSteps steps.  This schedule runs on the eight-wave
+// core, the data-parallel kernel on the faster four-wave core (K % 64 == 0),
+// so it is planned only while the tiles leave most CUs idle: at N = 4096,
+// K = 12288 (MI355X, 256 CUs, us data-parallel / eight-wave stream-K)
+// M = 512 (32 tiles): 263 / 169, 2048 (128): 270 / 219, 2560 (160): 274 /
+// 250, 2816 (176): 279 / 267, 3100 (208): 252 / 269 -- up to 11/16 of the
+// CUs; beyond that the four-wave core's own stream-K schedule (w4sk_plan)
+// takes long-K shapes.
 constexpr int kSkMinSteps = 16;
 constexpr int kSkMinMain = 192;
 constexpr int kSkMaxTileShare16 = 11;  // tiles <= CUs * 11 / 16
