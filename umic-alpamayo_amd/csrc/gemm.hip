@@ -1962,7 +1962,8 @@ struct SkPlan {
 // tails' per-piece prologues and partial stores.  Measured on MI355X at
 // M = 3100, N = 4096, in one process against the data-parallel four-wave
 // kernel: down_proj (K = 12288, 208 tiles, Gt = 48) 228-234 against 234-242
-// us over ks = 160..165 (157: no gain, 170+: slower); q/o (K = 4096)
+// us over ks = 160..165 (157: no gain, 170+: slower; fewer tails, Gt = 40
+// .. 16, slower step by step: 234 .. 249 against 230 us); q/o (K = 4096)
 // 95-99 against 87-89 us at every ks tried -- the partials' stores and the
 // main workgroup's device-scope reads cost more than the idle CUs return,
 // so the schedule needs kW4SkMinKT stages.
