@@ -1245,6 +1245,9 @@ struct W4SkArgs {
 };
 constexpr int kW4SlotVec = 64 * kW4Threads;  // f32x4 per partial (256 KB)
 constexpr int kW4SkFlag = 150 * 1024;        // LDS word past the staged output
+static_assert(kW4SkFlag >= kBM * W4Tile<1>::kOutRow && kW4SkFlag + 4 <= kW4LdsBytes &&
+                  kW4SkFlag >= 2 * kW4StageBytes,
+              "the wait flag lies past the staged output and the K-loop stages");
 
 // Tail workgroup owning unit v, and tail j's first unit.
 __device__ __forceinline__ int w4sk_owner(int64_t v, int64_t Ut, int Gt) {
