@@ -1215,9 +1215,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs g, SkArgs
 
 // ---- Stream-K on the four-wave core ---------------------------------------
 //
-// For K % 64 == 0 and tiles that fill most but not all CUs (M = 3100 at
-// N = 4096: 208 tiles on 256 CUs), the data-parallel four-wave kernel leaves
-// the remaining CUs idle.  Here Gt "tail" workgroups (a multiple of 8, at
+// For K % 64 == 0, a long K loop (K >= 8192, w4sk_plan) and tiles that fill
+// most but not all CUs (down_proj at M = 3100: 208 tiles on 256 CUs), the
+// data-parallel four-wave kernel leaves the remaining CUs idle.  Here Gt
+// "tail" workgroups (a multiple of 8, at
 // most T) take the last L = KT - ks stages of every tile while T "main"
 // workgroups run the first ks stages of one tile each, in lockstep as in the
 // data-parallel kernel.  Tail j owns units [j*Ut/Gt, (j+1)*Ut/Gt) of the
