@@ -203,6 +203,19 @@ def test_four_wave_stream_k_close_to_data_parallel(M, N, K):
     assert max_rel_err(y1, ref) <= TOL
 
 
+def test_four_wave_stream_k_workspace_layout():
+    """The schedule's workspace: the 16,640-byte counter region (tile
+    counters, status word, the few-tile schedule's slot tags), then one
+    256 KB slot per tail piece, T + Gt - 1 of them, Gt = min(T, CUs - T
+    rounded up to 8) rounded down to 8 tails; K below 8192 takes none."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for M, N, K in W4SK_SHAPES:
+        T = -(-M // 256) * -(-N // 256)
+        gt = min(T, cus - -(-T // 8) * 8) // 8 * 8
+        assert _sk_bytes(M, N, K) == 16640 + (T + gt - 1) * 256 * 1024, (M, N, K)
+    assert _sk_bytes(3100, 4096, 4096) == 0  # q/o: the data-parallel kernel
+
+
 @pytest.mark.parametrize("act,code", [("gelu", 1), ("gelu_tanh", 2)])
 def test_four_wave_stream_k_bias_gelu(act, code):
     """The bias + GELU epilogue after the partial sums, against the
