@@ -406,6 +406,17 @@ int umic_add_rmsnorm_gate_silu_mul_bf16(const void* x, const void* r, const void
 #define UMIC_STREAM_READ_GRID 2048
 int umic_stream_read(const void* p, int64_t bytes, void* fold, void* stream);
 
+/*
+ * Measurement helper: copies `bytes` bytes from src to dst (16-byte
+ * non-temporal loads and stores, one-shot grid; both 16-byte aligned and
+ * bytes a multiple of 16, else UMIC_ERR_UNSUPPORTED; overlapping ranges
+ * UMIC_ERR_INVALID_ARG).  Its time is the practical ceiling of a kernel that
+ * reads bytes once and writes bytes once, the yardstick bench.py holds the
+ * norm and RoPE kernels against.  No counterpart in the reference; nothing
+ * on the fused path calls it.
+ */
+int umic_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,7 +39,7 @@ def test_header_declares_expected_entry_points():
               "umic_linear_multi_bf16", "umic_linear_add_bf16",
               "umic_rope_kv_append_bf16", "umic_qk_rmsnorm_rope_bf16",
               "umic_qk_rmsnorm_rope_kv_append_bf16", "umic_linear_sk_static_bf16",
-              "umic_stream_read", "umic_version", "umic_error_string"):
+              "umic_stream_read", "umic_stream_copy", "umic_version", "umic_error_string"):
         assert n in names
 
 
@@ -115,6 +115,15 @@ def test_argument_rejection_before_launch(lib):
     assert rd(None, 4096, fake, None) == E_ARG
     assert rd(fake, 4100, fake, None) == E_UNS
     assert rd(fake + 8, 4096, fake, None) == E_UNS
+    # the copy-ceiling helper: the same, and overlapping ranges
+    cp = lib.umic_stream_copy
+    assert cp(fake, fake + 8192, -16, None) == E_ARG
+    assert cp(None, None, 0, None) == 0
+    assert cp(None, fake, 4096, None) == E_ARG
+    assert cp(fake, fake + 2048, 4096, None) == E_ARG
+    assert cp(fake + 4096, fake, 4096 + 16, None) == E_ARG
+    assert cp(fake, fake + 8192, 4100, None) == E_UNS
+    assert cp(fake, fake + 8200, 4096, None) == E_UNS
     assert lib.umic_gate_silu_mul_bf16(fake, fake, None, fake, 8, 64, 128, 128, 128, 128, 64,
                                        None) == E_ARG
     # stream-K linear: same validation; a negative workspace size is rejected

@@ -1,4 +1,5 @@
-"""GPU: umic_stream_read reads every byte it is given, once.
+"""GPU: umic_stream_read reads every byte it is given, once; umic_stream_copy
+copies every byte it is given and nothing past them.
 
 The read-ceiling helper xor-folds what each workgroup reads into one word
 per workgroup.  XOR is associative and commutative, so the xor of all fold
@@ -6,7 +7,10 @@ words equals the xor of every 32-bit word of the buffer, whatever the grid
 walk.  A skipped 16-byte load drops its words from the fold and a doubled
 one cancels them, so either changes the fold of random data.  Sizes cover a
 partial last trip of the grid, a buffer smaller than one trip, and one
-16-byte load.
+16-byte load.  The copy's destination carries a guard band of a known
+pattern past its end that must survive; its sizes cover a partial last
+workgroup (512 16-byte loads each), a partial last lane pair, one load, and
+a BASELINE-sized side.
 """
 
 from __future__ import annotations
@@ -42,3 +46,27 @@ def test_misaligned_and_ragged_sizes_are_rejected():
     assert rd(buf.data_ptr(), 20, fold.data_ptr(), st) == _lib.UMIC_ERR_UNSUPPORTED
     assert rd(buf.data_ptr() + 4, 32, fold.data_ptr(), st) == _lib.UMIC_ERR_UNSUPPORTED
     assert rd(buf.data_ptr(), 0, fold.data_ptr(), st) == _lib.UMIC_OK
+
+
+@pytest.mark.parametrize("nbytes", [16, 512 * 16 * 3 + 16 * 257, 512 * 16 * 5 + 16, 25_399_296])
+def test_copy_is_exact_and_stays_in_its_range(nbytes):
+    print(f"umic_stream_copy bytes={nbytes}", flush=True)
+    guard = 4096
+    g = torch.Generator(device="cpu").manual_seed(nbytes)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g).to(DEV)
+    dst = torch.full((nbytes + guard,), 0xA5, dtype=torch.uint8, device=DEV)
+    _lib.call("umic_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, _lib.stream_of(src))
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert bool((dst[nbytes:] == 0xA5).all())
+
+
+def test_copy_rejections():
+    buf = torch.zeros(1024, dtype=torch.int32, device=DEV)
+    cp = _lib.lib().umic_stream_copy
+    st = _lib.stream_of(buf)
+    p = buf.data_ptr()
+    assert cp(p, p + 2048, 1000, st) == _lib.UMIC_ERR_UNSUPPORTED
+    assert cp(p, p + 2052, 1024, st) == _lib.UMIC_ERR_UNSUPPORTED
+    assert cp(p, p + 1024, 2048, st) == _lib.UMIC_ERR_INVALID_ARG
+    assert cp(p, p + 2048, 0, st) == _lib.UMIC_OK

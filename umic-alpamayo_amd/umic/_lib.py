@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "umic_linear_ws_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P],
     "umic_linear_sk_static_bf16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     "umic_stream_read": [_P, _I64, _P, _P],
+    "umic_stream_copy": [_P, _P, _I64, _P],
     "umic_version": [],
     "umic_error_string": [_I],
 }
