@@ -590,28 +590,45 @@ COPY_BYTES = 512 << 20
 
 def copy_ceiling() -> int:
     """Practical HBM ceiling at the norm/RoPE sizes: torch's own device copy
-    (read n, write n) of the same byte counts, back-to-back over 12 buffers."""
+    (read n, write n) of the same byte counts, back-to-back over 12 buffers,
+    then the library's streaming copy (umic_stream_copy) over the same
+    buffers; each timed group queued behind two spacer GEMMs so the host's
+    launch cost stays out of the events."""
     import torch
 
+    from umic import _lib
+
     torch.cuda.set_device(0)
+    _lib.load()
+    sa = torch.randn(8192, 8192, device="cuda").to(torch.bfloat16)
+
+    def timed(fn, nbuf):
+        for i in range(nbuf):
+            fn(i)
+        torch.cuda.synchronize()
+        sa @ sa
+        sa @ sa
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(nbuf):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / nbuf * 1e3
+
     for moved in (50_798_592, 83_891_200, 101_588_992, 167_777_280, 178_257_920,
                   400_000_000, 2 << 30):
         n = moved // 4  # bf16 elements per side
         nbuf = 12 if moved < (1 << 30) else 3
         src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(nbuf)]
         dst = [torch.empty_like(src[0]) for _ in range(nbuf)]
-        for i in range(nbuf):
-            dst[i].copy_(src[i])
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(nbuf):
-            dst[i].copy_(src[i])
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / nbuf * 1e3
+        st = _lib.stream_of(src[0])
+        us = timed(lambda i: dst[i].copy_(src[i]), nbuf)
+        sus = timed(lambda i: _lib.call("umic_stream_copy", src[i].data_ptr(), dst[i].data_ptr(),
+                                        moved // 2, st), nbuf)
         print(json.dumps({"copy_bytes_moved": moved, "us": round(us, 2),
-                          "gbps": round(moved / us / 1e3, 1)}), flush=True)
+                          "gbps": round(moved / us / 1e3, 1), "stream_copy_us": round(sus, 2),
+                          "stream_copy_gbps": round(moved / sus / 1e3, 1)}), flush=True)
         del src, dst
     return 0
 
