@@ -87,6 +87,36 @@ def test_decoder_layer_prefill_and_decode(M, call_log):
         assert call_log["umic_linear_ws_bf16"] == 1 and call_log["umic_linear_bf16"] == 0
 
 
+def test_decoder_layer_prefill_with_tiled_qo(call_log, monkeypatch):
+    """Prefill with the reference's own q/o rule (the tiled kernel from 64
+    rows, src/umic/integrate.py:91,98-131): q_proj and o_proj
+    then run on this library's tiled linear beside down_proj, and the layer
+    still matches the unpatched one within the GEMM tolerance."""
+    monkeypatch.setattr(integrate, "TILED_MIN_ROWS_LINEAR", 64)
+    M = 3100
+    layer, rot = decoder_layer()
+    torch.manual_seed(1)
+    h = torch.randn(1, M, 4096).to(torch.bfloat16).to(DEV)
+    pos = torch.arange(M, device=DEV)[None]
+    cos_sin = rot(h, pos)
+    with torch.no_grad():
+        ref = layer(h, position_embeddings=cos_sin)
+        assert integrate.fuse_mlps(layer) == 1
+        assert integrate.fuse_linears(layer) == 2
+        assert integrate.fuse_rmsnorms(layer) == 4
+        assert integrate.fuse_add_rmsnorm(layer) == 1
+        assert integrate.fuse_text_rope()
+        out = layer(h, position_embeddings=cos_sin)
+        torch.cuda.synchronize()
+    e1, e2 = max_rel_err(out, ref), rel_err(out, ref)
+    print(f"decoder layer M={M}, tiled q/o: max_rel {e1:.2e} rel {e2:.2e} calls "
+          f"{dict(call_log)}", flush=True)
+    assert e1 <= TOL and e2 <= TOL
+    # q_proj, o_proj and down_proj on the tiled linear
+    assert call_log["umic_linear_ws_bf16"] + call_log["umic_linear_bf16"] == 3
+    assert call_log["umic_gate_silu_mul_bf16"] == 1
+
+
 def test_decoder_layer_with_autograd_runs_eager(call_log):
     """Grad mode on and weights requiring grad: the patched layer makes no
     kernel call (the kernels have no backward) and equals the unpatched layer
