@@ -65,6 +65,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -854,9 +855,11 @@ def layer_step() -> dict:
     norms 1 + N(0, 0.1)) timed eager and with the fused path injected
     (fuse_mlps, fuse_linears, fuse_rmsnorms, fuse_add_rmsnorm, fuse_text_rope,
     fuse_kv_rope -- with no cache, q_norm / k_norm / RoPE in one launch):
-    prefill at M=3100 and decode at M=1, the decode step also captured in a
-    HIP graph (torch.cuda.CUDAGraph) and replayed, as the reference's decode
-    runner does (src/umic/graph.py:155-167)."""
+    prefill at M=3100 (also with the reference's q/o rule, the tiled linear
+    from 64 rows: prefill_M3100_umic_tiled_qo_ms) and decode at M=1, the
+    decode step also captured in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed, as the reference's decode runner does
+    (src/umic/graph.py:155-167)."""
     import torch
 
     from umic import integrate
@@ -883,7 +886,10 @@ def layer_step() -> dict:
     with torch.no_grad():
         run = {M: (lambda h=h, cs=cs: layer(h, position_embeddings=cs))
                for M, (h, cs) in inputs.items()}
-        res["prefill_M3100_eager_ms"] = round(timed(run[3100], 10) / 1e3, 4)
+        for _ in range(10):
+            run[3100]()
+        res["prefill_M3100_eager_ms"] = round(
+            statistics.median(timed(run[3100], 10) for _ in range(3)) / 1e3, 4)
         res["decode_M1_eager_us"] = round(timed(run[1], 200), 1)
         integrate.fuse_mlps(layer)
         integrate.fuse_linears(layer)
@@ -891,8 +897,22 @@ def layer_step() -> dict:
         integrate.fuse_add_rmsnorm(layer)
         integrate.fuse_text_rope()
         integrate.fuse_kv_rope(layer)
+        saved_qo = integrate.TILED_MIN_ROWS_LINEAR
         try:
-            res["prefill_M3100_umic_ms"] = round(timed(run[3100], 10) / 1e3, 4)
+            # the fused prefill with this build's q/o choice and with the
+            # reference's q/o rule (the tiled linear from 64 rows),
+            # interleaved three times each after a warm-up (the first timed
+            # group after injection read ~5% slow): medians
+            for _ in range(10):
+                run[3100]()
+            pre = {saved_qo: [], 64: []}
+            for r in range(6):
+                rule = (saved_qo, 64)[r % 2]
+                integrate.TILED_MIN_ROWS_LINEAR = rule
+                pre[rule].append(timed(run[3100], 10))
+            integrate.TILED_MIN_ROWS_LINEAR = saved_qo
+            res["prefill_M3100_umic_ms"] = round(statistics.median(pre[saved_qo]) / 1e3, 4)
+            res["prefill_M3100_umic_tiled_qo_ms"] = round(statistics.median(pre[64]) / 1e3, 4)
             res["decode_M1_umic_us"] = round(timed(run[1], 200), 1)
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -904,6 +924,7 @@ def layer_step() -> dict:
                 run[1]()
             res["decode_M1_umic_graph_us"] = round(timed(graph.replay, 200), 1)
         finally:
+            integrate.TILED_MIN_ROWS_LINEAR = saved_qo
             integrate.unfuse_mlps(layer)
             integrate.unfuse_rope()
     return res
