@@ -136,3 +136,34 @@ def test_stream_k_workspace_outlives_a_captured_graph():
         assert torch.equal(out, ref)
         assert bool((sentinel == 0x5A).all())
     assert big.shape == (2816, 4096)
+
+
+def test_four_wave_stream_k_replays_in_hip_graph():
+    """The four-wave stream-K schedule (the down_proj path: K >= 8192 and
+    most CUs' worth of tiles) captured in a HIP graph: its tile counters are
+    left at zero by each launch, so replays on fresh inputs equal the eager
+    call bit for bit, with eager launches on the same workspace between
+    them."""
+    g = torch.Generator().manual_seed(11)
+    x = bf16_randn(3100, 8192, gen=g).to(DEV)
+    w = bf16_randn(4096, 8192, scale=0.02, gen=g).to(DEV)
+    assert linear.stream_k_planned(x, w)
+    print("four-wave stream-K graph capture M=3100 N=4096 K=8192", flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        linear.linear_hip(x, w)                   # this stream's workspace
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = linear.linear_hip(x, w)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for seed in range(3):
+        gi = torch.Generator().manual_seed(100 + seed)
+        x.copy_(bf16_randn(3100, 8192, gen=gi).to(DEV))
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            graph.replay()
+            ref = linear.linear_hip(x, w)         # eager, same stream and workspace
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), seed
