@@ -104,11 +104,14 @@ def test_shape_beyond_the_scratch_is_rejected():
     assert not out.any()  # nothing ran
 
 
-def test_static_scratch_under_graph_capture():
+@pytest.mark.parametrize("M", [300, 3100])
+def test_static_scratch_under_graph_capture(M):
     """The static entry point captured in a HIP graph (its callers are code
     under capture): every replay, with new inputs copied in and eager work
-    between replays, equals the workspace entry point bit for bit."""
-    M, N, K = 300, 4096, 12288
+    between replays, equals the workspace entry point bit for bit -- on the
+    eight-wave stream-K schedule (M = 300) and the four-wave one (the
+    BASELINE down_proj, M = 3100)."""
+    N, K = 4096, 12288
     print(f"static stream-K graph capture M={M} N={N} K={K}", flush=True)
     x, w, _ = _operands(M, N, K, 5)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
